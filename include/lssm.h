@@ -1,0 +1,317 @@
+/*
+ * lssm.h — C ABI of the MI355X (gfx950) Mamba-2 inference backend.
+ *
+ * This is the drop-in boundary that replaces the Metal backend of lite-ssm
+ * (src/backend/metal/ops.mm and the shaders/ directory).  Every entry point takes plain
+ * device pointers and sizes; nothing here names a torch or Metal type.
+ *
+ *   - Each reference dispatcher `MetalOps::<op>` (include/lite_ssm/ops.hpp:99-235)
+ *     has a same-named `lssm_<op>` entry below with the same argument meaning.
+ *     A MetalOps (handle, byte_offset) pair becomes one pointer, handle + offset.
+ *   - The generic entries (`lssm_linear`, `lssm_ssd_chunked`, ...) add what the
+ *     reference cannot express: a batch dimension, bf16/fp32 activations, and
+ *     the Q4_G64 / Q8_G32 weight formats.  The reference-named entries are thin
+ *     wrappers over them with batch 1, fp16 activations and INT4_B32 weights.
+ *   - The engine entries (`lssm_engine_*`) run the whole per-layer op sequence
+ *     of Mamba2Model::run_block (src/model/mamba2_block.cpp:51-290) with fused
+ *     kernels, device-side embedding and argmax, and HIP-graph replay.
+ *
+ * Error model: every call returns an `int` status (LSSM_OK == 0).  On failure a
+ * thread-local message is available from lssm_last_error(); the C++ shim
+ * (include/lite_ssm/ops.hpp) rethrows it as std::runtime_error, mirroring the
+ * reference's throw sites (ops.mm:39-45, 83-85, 96-98, 107-110, 144-147).
+ *
+ * Execution model: every op is enqueued on the stream owned (or borrowed) by
+ * the lssm_ctx.  Outside a batch an op is synchronous (launch + stream sync +
+ * error check), like the reference's one-shot command buffer (ops.mm:131-148).
+ * Inside lssm_begin_batch / lssm_commit_and_wait ops only enqueue
+ * (ops.mm:82-112).
+ */
+#ifndef LSSM_H
+#define LSSM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------- */
+/* Status, dtypes, formats                                                    */
+/* ------------------------------------------------------------------------- */
+enum {
+    LSSM_OK        = 0,
+    LSSM_EINVAL    = 1,  /* bad argument / dimension precondition            */
+    LSSM_EDEVICE   = 2,  /* HIP runtime or kernel failure                    */
+    LSSM_ESTATE    = 3,  /* batch misuse (begin twice, commit without begin) */
+    LSSM_ENOTFOUND = 4   /* unknown kernel name                              */
+};
+
+/* Activation dtypes.  Codes match the .ssm dtype codes
+ * (include/lite_ssm/ssm_format.hpp:29-41): F16 = 0, BF16 = 1, F32 = 2. */
+typedef enum { LSSM_F16 = 0, LSSM_BF16 = 1, LSSM_F32 = 2 } lssm_dtype;
+
+/* Weight formats of a (N x K) row-major linear weight.
+ *   DENSE  : N*K elements of the activation dtype.
+ *   Q4_B32 : the reference DTYPE_INT4_B32 (ssm_format.hpp:36-43, 64-69):
+ *            [N*K/2 packed nibbles][N*K/32 fp16 scales]; low nibble = even k.
+ *   Q4_G64 : same layout, 64-element groups  -> [N*K/2][N*K/64 fp16].
+ *   Q8_G32 : int8 two's complement, 32-element groups -> [N*K][N*K/32 fp16].
+ * Q4_G64 and Q8_G32 are this build's extension codes (7 and 8). */
+typedef enum {
+    LSSM_W_DENSE  = 0,
+    LSSM_W_Q4_B32 = 6,
+    LSSM_W_Q4_G64 = 7,
+    LSSM_W_Q8_G32 = 8
+} lssm_wfmt;
+
+/* Epilogue applied to a linear output before the single rounding store.
+ *   NONE : y = r(acc)
+ *   SILU : y = r(silu(acc))
+ *   ADD  : y = r(residual + r(acc))   (out_proj + residual add, activations.metal:24-32)
+ * r() rounds to the activation dtype. */
+typedef enum { LSSM_EPI_NONE = 0, LSSM_EPI_SILU = 1, LSSM_EPI_ADD = 2 } lssm_epilogue;
+
+typedef struct lssm_ctx lssm_ctx;
+
+/* ------------------------------------------------------------------------- */
+/* Dims structs: field-for-field the reference's (ops.hpp:30-55, 193-202)     */
+/* ------------------------------------------------------------------------- */
+typedef struct { uint32_t M, N, K; } lssm_linear_dims;                 /* LinearDims    */
+typedef struct { uint32_t rows, dim; float eps; } lssm_rmsnorm_dims;   /* RMSNormDims   */
+typedef struct { uint32_t N, K; float eps; } lssm_rms_linear_dims;     /* RMSLinearDims */
+typedef struct { uint32_t B, L, D, K; } lssm_conv1d_dims;              /* Conv1dDims    */
+typedef struct {                                                       /* SSDDims       */
+    uint32_t L, H, P, N, n_groups, chunk_size;
+    float dt_min, dt_max;
+    uint32_t has_D;
+} lssm_ssd_dims;
+typedef struct {                                                       /* SSDStepDims   */
+    uint32_t H, P, N, n_groups;
+    float dt_min, dt_max;
+    uint32_t has_D;
+} lssm_ssd_step_dims;
+typedef struct {                                        /* MetalOps::FusedInProjDims */
+    uint32_t L, d_model, d_inner, d_state, n_groups, n_heads, d_conv, proj_dim;
+} lssm_fused_inproj_dims;
+
+/* ------------------------------------------------------------------------- */
+/* Context, batching, introspection                                           */
+/* ------------------------------------------------------------------------- */
+const char* lssm_last_error(void);
+
+/* `stream` = an existing hipStream_t to borrow, or NULL to create one.
+ * Replaces MetalOps::MetalOps() (ops.mm:62) and the queue singleton
+ * (metal_context.mm:25-70). */
+int lssm_ctx_create(lssm_ctx** out, void* stream);
+int lssm_ctx_destroy(lssm_ctx* ctx);
+int lssm_ctx_stream(lssm_ctx* ctx, void** stream_out);
+
+int lssm_begin_batch(lssm_ctx* ctx);       /* MetalOps::begin_batch   ops.hpp:91 */
+int lssm_commit_and_wait(lssm_ctx* ctx);   /* MetalOps::commit_and_wait ops.hpp:92 */
+int lssm_batch_active(lssm_ctx* ctx);      /* MetalOps::batch_active  ops.hpp:93 */
+int lssm_sync(lssm_ctx* ctx);              /* stream sync + error check          */
+
+/* MetalOps::metallib_loaded / has_pipeline / metallib_path (ops.hpp:66-74). */
+int lssm_library_loaded(void);
+int lssm_has_kernel(const char* name);
+const char* lssm_library_path(void);
+int lssm_kernel_count(void);
+const char* lssm_kernel_name(int i);
+
+/* Device memory plumbing (DeviceBuffer bodies, metal_buffer.mm:107-143). */
+int lssm_malloc(void** out, size_t nbytes);
+int lssm_malloc_managed(void** out, size_t nbytes);
+int lssm_free(void* p);
+int lssm_memcpy_h2d(lssm_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int lssm_memcpy_d2h(lssm_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int lssm_memcpy_d2d(lssm_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int lssm_memset(lssm_ctx* ctx, void* dst, int value, size_t nbytes);
+
+/* ------------------------------------------------------------------------- */
+/* Reference-named ops (fp16 activations, batch 1): one per MetalOps method    */
+/* ------------------------------------------------------------------------- */
+/* ops.hpp:99-102 */
+int lssm_rmsnorm_f16(lssm_ctx* ctx, const void* x, const void* w, void* y,
+                     lssm_rmsnorm_dims dims);
+/* ops.hpp:104-107 */
+int lssm_linear_f16_gemv(lssm_ctx* ctx, const void* x, const void* w, void* y,
+                         lssm_linear_dims dims);
+/* ops.hpp:109-112 */
+int lssm_linear_silu_f16_gemv(lssm_ctx* ctx, const void* x, const void* w, void* y,
+                              lssm_linear_dims dims);
+/* ops.hpp:114-118 */
+int lssm_rmsnorm_linear_f16_gemv(lssm_ctx* ctx, const void* x, const void* w_norm,
+                                 const void* w, void* y, lssm_rms_linear_dims dims);
+/* ops.hpp:120-123 */
+int lssm_linear_f16_gemm(lssm_ctx* ctx, const void* x, const void* w, void* y,
+                         lssm_linear_dims dims);
+/* ops.hpp:125-128 */
+int lssm_linear_silu_f16_gemm(lssm_ctx* ctx, const void* x, const void* w, void* y,
+                              lssm_linear_dims dims);
+/* ops.hpp:135-139 */
+int lssm_linear_int4_gemv(lssm_ctx* ctx, const void* x, const void* w_packed,
+                          const void* w_scales, void* y, lssm_linear_dims dims);
+/* ops.hpp:141-145 */
+int lssm_linear_int4_gemm(lssm_ctx* ctx, const void* x, const void* w_packed,
+                          const void* w_scales, void* y, lssm_linear_dims dims);
+/* ops.hpp:147-149 */
+int lssm_silu_f16(lssm_ctx* ctx, const void* x, void* y, uint32_t n);
+/* ops.hpp:151-153 */
+int lssm_add_inplace_f16(lssm_ctx* ctx, void* y, const void* x, uint32_t n);
+/* ops.hpp:158-163 */
+int lssm_split_silu_xBC_f16(lssm_ctx* ctx, const void* xBC, void* x_out, void* B_out,
+                            void* C_out, uint32_t L, uint32_t d_inner, uint32_t d_state,
+                            uint32_t n_groups);
+/* ops.hpp:165-168 */
+int lssm_silu_gated_f16(lssm_ctx* ctx, const void* x, const void* gate, void* y, uint32_t n);
+/* ops.hpp:170-174 */
+int lssm_causal_conv1d_f16(lssm_ctx* ctx, const void* x, const void* w, const void* bias,
+                           void* y, lssm_conv1d_dims dims);
+/* ops.hpp:176-181 */
+int lssm_causal_conv1d_update_f16(lssm_ctx* ctx, const void* x_new, void* state,
+                                  const void* w, const void* bias, void* y,
+                                  lssm_conv1d_dims dims);
+/* ops.hpp:186-188 */
+int lssm_seed_conv_state_f16(lssm_ctx* ctx, const void* xBC, void* state,
+                             uint32_t L, uint32_t D, uint32_t K);
+/* ops.hpp:203-213 */
+int lssm_inproj_fused_f16(lssm_ctx* ctx, const void* normed, const void* W_in,
+                          const void* W_conv, const void* conv_b, void* proj_z,
+                          void* ssd_x, void* ssd_B, void* ssd_C, void* proj_dt,
+                          void* proj_xBC, lssm_fused_inproj_dims dims);
+/* ops.hpp:215-224 */
+int lssm_ssd_chunked_f16(lssm_ctx* ctx, const void* X, const void* B, const void* C,
+                         const void* dt_raw, const void* dt_bias, const void* A_log,
+                         const void* D_skip, void* Y, float* state_io, lssm_ssd_dims dims);
+/* ops.hpp:226-235 */
+int lssm_ssd_step_f16(lssm_ctx* ctx, const void* x, const void* B, const void* C,
+                      const void* dt_raw, const void* dt_bias, const void* A_log,
+                      const void* D_skip, float* state, void* y, lssm_ssd_step_dims dims);
+
+/* ------------------------------------------------------------------------- */
+/* Generic ops (batch / dtype / format aware)                                 */
+/* ------------------------------------------------------------------------- */
+/* y[rows,dim] = r(x * w * rsqrt(mean(x^2) + eps))            norm.metal:52-79 */
+int lssm_rmsnorm(lssm_ctx* ctx, const void* x, const void* w, void* y,
+                 uint32_t rows, uint32_t dim, float eps, lssm_dtype act);
+
+/* Y[M,N] = epi(X[M,K] . deq(W)[N,K]^T).  `w_scales` is ignored for DENSE.
+ * `residual` is read only for EPI_ADD and may alias `y` (in-place residual).
+ * M <= 4 runs the GEMV kernel (fp32 dequant, linear.metal:440-474 semantics);
+ * larger M runs the MFMA GEMM, whose dequantized operand is rounded to the
+ * activation dtype (linear.metal:538 semantics).  x_stride/y_stride are row
+ * strides in elements (0 = packed). */
+int lssm_linear(lssm_ctx* ctx, const void* x, uint32_t x_stride,
+                const void* w, const void* w_scales,
+                void* y, uint32_t y_stride, const void* residual,
+                uint32_t M, uint32_t N, uint32_t K,
+                lssm_wfmt wfmt, lssm_dtype act, lssm_epilogue epi);
+
+/* Bit-exact dequantization of a whole (N x K) weight into fp32 (debug/parity). */
+int lssm_dequant(lssm_ctx* ctx, const void* w, const void* w_scales, float* out,
+                 uint32_t N, uint32_t K, lssm_wfmt wfmt);
+
+int lssm_silu(lssm_ctx* ctx, const void* x, void* y, uint32_t n, lssm_dtype act);
+int lssm_add_inplace(lssm_ctx* ctx, void* y, const void* x, uint32_t n, lssm_dtype act);
+int lssm_silu_gated(lssm_ctx* ctx, const void* x, const void* gate, void* y, uint32_t n,
+                    lssm_dtype act);
+int lssm_split_silu_xbc(lssm_ctx* ctx, const void* xBC, void* x_out, void* B_out,
+                        void* C_out, uint32_t rows, uint32_t d_inner, uint32_t d_state,
+                        uint32_t n_groups, lssm_dtype act);
+
+/* Depthwise causal conv, x/y [B, L, D], w [D, K], bias [D], zero left pad. */
+int lssm_conv1d(lssm_ctx* ctx, const void* x, const void* w, const void* bias, void* y,
+                uint32_t B, uint32_t L, uint32_t D, uint32_t K, lssm_dtype act);
+/* One decode step: x_new [B, D], state [B, D, K] (oldest first) updated in place. */
+int lssm_conv1d_update(lssm_ctx* ctx, const void* x_new, void* state, const void* w,
+                       const void* bias, void* y, uint32_t B, uint32_t D, uint32_t K,
+                       lssm_dtype act);
+/* state[b, d, k] = xBC[b, L-K+k, d] (0 where L-K+k < 0). */
+int lssm_conv1d_seed(lssm_ctx* ctx, const void* xBC, void* state, uint32_t B, uint32_t L,
+                     uint32_t D, uint32_t K, lssm_dtype act);
+
+/* out = r(rmsnorm(r(silu(z) * y), w))  — gate-then-norm (mamba2_block.cpp:230-238). */
+int lssm_gated_rmsnorm(lssm_ctx* ctx, const void* z, const void* y, const void* w,
+                       void* out, uint32_t rows, uint32_t dim, float eps, lssm_dtype act);
+
+/* Chunked SSD prefill over `batch` independent sequences of length dims.L.
+ * X/Y [batch, L, H, P]; B/C [batch, L, G, N]; dt_raw [batch, L, H];
+ * dt_bias/A_log/D [H] (act dtype); state [batch, H, P, N] fp32 in/out. */
+int lssm_ssd_chunked(lssm_ctx* ctx, const void* X, const void* B, const void* C,
+                     const void* dt_raw, const void* dt_bias, const void* A_log,
+                     const void* D_skip, void* Y, float* state, uint32_t batch,
+                     lssm_ssd_dims dims, lssm_dtype act);
+/* One decode step for `batch` sequences: x [batch, H, P], B/C [batch, G, N],
+ * dt_raw [batch, H], state [batch, H, P, N] fp32 updated in place. */
+int lssm_ssd_step(lssm_ctx* ctx, const void* x, const void* B, const void* C,
+                  const void* dt_raw, const void* dt_bias, const void* A_log,
+                  const void* D_skip, float* state, void* y, uint32_t batch,
+                  lssm_ssd_step_dims dims, lssm_dtype act);
+
+/* hidden[i, :] = table[ids[i], :]  (Mamba2Model::embed, mamba2_model.cpp:128-137). */
+int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out,
+               uint32_t n, uint32_t d_model, uint32_t vocab, lssm_dtype act);
+/* ids[r] = first index of the max of logits[r, :]  (sampler.cpp:13-21). */
+int lssm_argmax(lssm_ctx* ctx, const void* logits, int32_t* ids, uint32_t rows,
+                uint32_t vocab, lssm_dtype act);
+
+/* ------------------------------------------------------------------------- */
+/* Engine: whole-model prefill / decode (configs 3-5)                         */
+/* ------------------------------------------------------------------------- */
+typedef struct {
+    uint32_t d_model, n_layer, d_state, d_conv, expand, vocab_size;
+    uint32_t n_heads, d_head, chunk_size, n_groups;
+    uint32_t act;        /* lssm_dtype of activations and dense / 1-D params   */
+    uint32_t wfmt;       /* lssm_wfmt of in_proj / out_proj                     */
+} lssm_model_config;
+
+/* Device pointers of one layer's tensors (names as in the .ssm file,
+ * mamba2_model.cpp:62-116).  in_proj rows are [z | xBC | dt]. */
+typedef struct {
+    const void* norm_w;        /* [d_model]                     */
+    const void* in_proj_w;     /* packed (or dense) [proj_dim, d_model] */
+    const void* in_proj_s;     /* fp16 scales or NULL           */
+    const void* conv1d_w;      /* [xBC_dim, d_conv]             */
+    const void* conv1d_b;      /* [xBC_dim]                     */
+    const void* dt_bias;       /* [n_heads]                     */
+    const void* A_log;         /* [n_heads]                     */
+    const void* D;             /* [n_heads]                     */
+    const void* mixer_norm_w;  /* [d_inner]                     */
+    const void* out_proj_w;    /* [d_model, d_inner]            */
+    const void* out_proj_s;
+} lssm_layer_weights;
+
+typedef struct lssm_engine lssm_engine;
+
+/* `layers` has cfg->n_layer entries; embed is [vocab, d_model], lm_head may
+ * equal embed (tied).  The engine keeps the pointers (caller owns memory). */
+int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config* cfg,
+                       const void* embed, const void* norm_f, const void* lm_head,
+                       const lssm_layer_weights* layers,
+                       uint32_t max_batch, uint32_t max_seq);
+int lssm_engine_destroy(lssm_engine* e);
+/* Zero conv + SSD state of all sequences (Mamba2State::reset, state.cpp:49-51). */
+int lssm_engine_reset(lssm_engine* e);
+/* Prefill `batch` sequences of `L` token ids each (device int32 [batch, L]).
+ * Writes last-position fp-act logits to the logits buffer and greedy ids to
+ * `next_ids` (device int32 [batch]). */
+int lssm_engine_prefill(lssm_engine* e, const int32_t* ids, uint32_t batch, uint32_t L,
+                        int32_t* next_ids);
+/* One decode step for `batch` sequences: reads ids (device int32 [batch]),
+ * writes logits and greedy next ids (device, may alias ids). */
+int lssm_engine_decode(lssm_engine* e, const int32_t* ids, uint32_t batch, int32_t* next_ids);
+/* Capture `lssm_engine_decode(ids, batch, next_ids)` into a HIP graph (replaces
+ * any earlier capture) and replay it `steps` times back to back. */
+int lssm_engine_decode_graph(lssm_engine* e, const int32_t* ids, uint32_t batch,
+                             int32_t* next_ids, uint32_t steps);
+/* Device pointers to engine buffers (valid until destroy). */
+int lssm_engine_logits(lssm_engine* e, void** logits);          /* [max_batch, vocab] act */
+int lssm_engine_state(lssm_engine* e, void** conv_state, void** ssd_state);
+/* conv_state: [n_layer, max_batch, xBC_dim, d_conv] act; ssd: [n_layer, max_batch, H, P, N] f32 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LSSM_H */

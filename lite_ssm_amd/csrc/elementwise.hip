@@ -1,0 +1,415 @@
+// elementwise.hip — RMSNorm, gated RMSNorm, SiLU family, depthwise causal
+// conv1d (prefill / decode update / state seed), embedding gather, argmax.
+//
+// Arithmetic follows shaders/norm.metal:52-79, activations.metal:12-87 and
+// conv1d.metal:35-137; storage is fp16 / bf16 / fp32, math fp32.
+#include <cfloat>
+
+#include "common.cuh"
+#include "internal.hpp"
+
+namespace lssm {
+
+#define LSSM_DISPATCH_ACT(act, T, ...)                   \
+    do {                                                 \
+        if ((act) == LSSM_F16) {                         \
+            using T = f16;                               \
+            __VA_ARGS__;                                 \
+        } else if ((act) == LSSM_BF16) {                 \
+            using T = bf16;                              \
+            __VA_ARGS__;                                 \
+        } else {                                         \
+            using T = float;                             \
+            __VA_ARGS__;                                 \
+        }                                                \
+    } while (0)
+
+constexpr int NT = 256;
+
+// norm.metal:52-79 — one block per row; y = r(x*w*rsqrt(mean(x^2)+eps)).
+template <typename T>
+__global__ __launch_bounds__(NT) void rmsnorm_kernel(const T* __restrict__ x, uint32_t xs,
+                                                     const T* __restrict__ w, T* __restrict__ y,
+                                                     uint32_t ys, uint32_t dim, float eps) {
+    __shared__ float red[NT / WAVE];
+    const T* xr = x + (size_t)blockIdx.x * xs;
+    T* yr = y + (size_t)blockIdx.x * ys;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < dim; i += NT) {
+        float v = to_f(xr[i]);
+        ss += v * v;
+    }
+    ss = block_sum<NT>(ss, red);
+    const float rrms = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (uint32_t i = threadIdx.x; i < dim; i += NT) yr[i] = from_f<T>(to_f(xr[i]) * to_f(w[i]) * rrms);
+}
+
+// activations.metal:76-87 then norm.metal:52-79 (gate-then-norm,
+// mamba2_block.cpp:230-238): g = r(silu(z)*y); out = r(g*w*rsqrt(mean g^2+eps)).
+template <typename T>
+__global__ __launch_bounds__(NT) void gated_rmsnorm_kernel(const T* __restrict__ z, uint32_t zs,
+                                                           const T* __restrict__ yv, uint32_t yst,
+                                                           const T* __restrict__ w,
+                                                           T* __restrict__ out, uint32_t dim,
+                                                           float eps) {
+    __shared__ float red[NT / WAVE];
+    const T* zr = z + (size_t)blockIdx.x * zs;
+    const T* yr = yv + (size_t)blockIdx.x * yst;
+    T* o = out + (size_t)blockIdx.x * dim;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < dim; i += NT) {
+        float g = rnd<T>(silu_f(to_f(zr[i])) * to_f(yr[i]));
+        ss += g * g;
+    }
+    ss = block_sum<NT>(ss, red);
+    const float rrms = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (uint32_t i = threadIdx.x; i < dim; i += NT) {
+        float g = rnd<T>(silu_f(to_f(zr[i])) * to_f(yr[i]));
+        o[i] = from_f<T>(g * to_f(w[i]) * rrms);
+    }
+}
+
+template <typename T>
+__global__ void silu_kernel(const T* __restrict__ x, T* __restrict__ y, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = from_f<T>(silu_f(to_f(x[i])));
+}
+
+template <typename T>
+__global__ void add_kernel(T* y, const T* __restrict__ x, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = from_f<T>(to_f(y[i]) + to_f(x[i]));
+}
+
+template <typename T>
+__global__ void silu_gated_kernel(const T* __restrict__ x, const T* __restrict__ g,
+                                  T* __restrict__ y, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = from_f<T>(silu_f(to_f(x[i])) * to_f(g[i]));
+}
+
+// activations.metal:49-73
+template <typename T>
+__global__ void split_silu_kernel(const T* __restrict__ xBC, T* __restrict__ xo,
+                                  T* __restrict__ Bo, T* __restrict__ Co, uint32_t rows,
+                                  uint32_t d_inner, uint32_t GN) {
+    const uint32_t dim = d_inner + 2u * GN;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * dim) return;
+    uint32_t t = (uint32_t)(i / dim), f = (uint32_t)(i % dim);
+    T v = from_f<T>(silu_f(to_f(xBC[i])));
+    if (f < d_inner) xo[(size_t)t * d_inner + f] = v;
+    else if (f < d_inner + GN) Bo[(size_t)t * GN + (f - d_inner)] = v;
+    else Co[(size_t)t * GN + (f - d_inner - GN)] = v;
+}
+
+// conv1d.metal:63-93 — y[b,t,d] = r(bias + sum_tap w[d,tap] x[b,t-(K-1-tap),d]),
+// zero left padding.  SILU additionally applies r(silu(.)) to the rounded conv
+// output (the split_silu pass fused in).
+template <typename T, bool SILU>
+__global__ void conv1d_kernel(const T* __restrict__ x, uint32_t xs, const T* __restrict__ w,
+                              const T* __restrict__ bias, T* __restrict__ y, uint32_t ys,
+                              uint32_t L, uint32_t D, uint32_t K) {
+    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = blockIdx.y;
+    const uint32_t b = blockIdx.z;
+    if (d >= D) return;
+    const size_t row0 = (size_t)b * L;
+    float acc = bias ? to_f(bias[d]) : 0.0f;
+    for (uint32_t tap = 0; tap < K; ++tap) {
+        int src = (int)t - (int)(K - 1 - tap);
+        float v = 0.0f;
+        if (src >= 0) v = to_f(x[(row0 + (uint32_t)src) * xs + d]);
+        acc += to_f(w[(size_t)d * K + tap]) * v;
+    }
+    float o = rnd<T>(acc);
+    if (SILU) o = silu_f(o);
+    y[(row0 + t) * ys + d] = from_f<T>(o);
+}
+
+// conv1d.metal:108-137 — shift the window left, append x, y = r(bias + sum s*w).
+template <typename T>
+__global__ void conv1d_update_kernel(const T* __restrict__ x_new, T* state, const T* __restrict__ w,
+                                     const T* __restrict__ bias, T* __restrict__ y, uint32_t D,
+                                     uint32_t K) {
+    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t b = blockIdx.y;
+    if (d >= D) return;
+    T* sd = state + ((size_t)b * D + d) * K;
+    const T* wd = w + (size_t)d * K;
+    for (uint32_t k = 0; k + 1 < K; ++k) sd[k] = sd[k + 1];
+    sd[K - 1] = x_new[(size_t)b * D + d];
+    float acc = bias ? to_f(bias[d]) : 0.0f;
+    for (uint32_t k = 0; k < K; ++k) acc += to_f(sd[k]) * to_f(wd[k]);
+    y[(size_t)b * D + d] = from_f<T>(acc);
+}
+
+// conv1d_update_kernel fused with SiLU, strided rows (engine decode, batch > 4):
+// y = r(silu(r(bias + sum s*w))).
+template <typename T>
+__global__ void conv1d_update_silu_kernel(const T* __restrict__ x_new, uint32_t xs, T* state,
+                                          const T* __restrict__ w, const T* __restrict__ bias,
+                                          T* __restrict__ y, uint32_t ys, uint32_t D, uint32_t K) {
+    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t b = blockIdx.y;
+    if (d >= D) return;
+    T* sd = state + ((size_t)b * D + d) * K;
+    const T* wd = w + (size_t)d * K;
+    for (uint32_t k = 0; k + 1 < K; ++k) sd[k] = sd[k + 1];
+    sd[K - 1] = x_new[(size_t)b * xs + d];
+    float acc = bias ? to_f(bias[d]) : 0.0f;
+    for (uint32_t k = 0; k < K; ++k) acc += to_f(sd[k]) * to_f(wd[k]);
+    y[(size_t)b * ys + d] = from_f<T>(silu_f(rnd<T>(acc)));
+}
+
+// Zero all but the newest tap of each window (the seed of a 1-token prefill,
+// conv1d.metal:45-50 with L = 1).
+template <typename T>
+__global__ void conv1d_keep_last_kernel(T* state, uint32_t n_windows, uint32_t K) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)n_windows * (K - 1)) return;
+    const size_t wdx = i / (K - 1), k = i % (K - 1);
+    state[wdx * K + k] = from_f<T>(0.0f);
+}
+
+// conv1d.metal:35-51 — state[b,d,k] = xBC[b, L-K+k, d] or 0.
+template <typename T>
+__global__ void conv1d_seed_kernel(const T* __restrict__ xBC, uint32_t xs, T* __restrict__ state,
+                                   uint32_t L, uint32_t D, uint32_t K) {
+    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t b = blockIdx.y;
+    if (d >= D) return;
+    for (uint32_t k = 0; k < K; ++k) {
+        int src = (int)L - (int)K + (int)k;
+        T v = from_f<T>(0.0f);
+        if (src >= 0) v = xBC[((size_t)b * L + (uint32_t)src) * xs + d];
+        state[((size_t)b * D + d) * K + k] = v;
+    }
+}
+
+// mamba2_model.cpp:128-137 on device; out-of-range ids write zeros (the host
+// API rejects them before launch; this only guards the device read).
+template <typename T>
+__global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restrict__ ids,
+                             T* __restrict__ out, uint32_t d_model, uint32_t vocab) {
+    const uint32_t i = blockIdx.y;
+    const int32_t id = ids[i];
+    const bool ok = id >= 0 && (uint32_t)id < vocab;
+    for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < d_model; c += gridDim.x * blockDim.x)
+        out[(size_t)i * d_model + c] = ok ? table[(size_t)id * d_model + c] : from_f<T>(0.0f);
+}
+
+// sampler.cpp:13-21: first index of the maximum.  (v, i) beats (v', i') iff
+// v > v' or (v == v' and i < i').
+__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+template <int NTHR>
+__device__ __forceinline__ void block_argmax(float& bv, int& bi) {
+    __shared__ float sv[NTHR / WAVE];
+    __shared__ int si[NTHR / WAVE];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float ov = __shfl_xor(bv, off, WAVE);
+        int oi = __shfl_xor(bi, off, WAVE);
+        argmax_merge(bv, bi, ov, oi);
+    }
+    const int wv = threadIdx.x / WAVE;
+    if ((threadIdx.x % WAVE) == 0) {
+        sv[wv] = bv;
+        si[wv] = bi;
+    }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+    for (int i = 1; i < NTHR / WAVE; ++i) argmax_merge(bv, bi, sv[i], si[i]);
+    __syncthreads();
+}
+
+// Stage 1: block (blk, row) reduces a slice.  Stage 2 (or single pass when
+// gridDim.x == 1) writes the id.
+template <typename T, int NTHR>
+__global__ __launch_bounds__(NTHR) void argmax_partial_kernel(const T* __restrict__ logits,
+                                                              uint32_t vocab, float* pv, int* pi,
+                                                              int32_t* ids) {
+    const uint32_t row = blockIdx.y;
+    const uint32_t per = (vocab + gridDim.x - 1) / gridDim.x;
+    const uint32_t lo = blockIdx.x * per;
+    const uint32_t hi = min(vocab, lo + per);
+    const T* lr = logits + (size_t)row * vocab;
+    float bv = -FLT_MAX;
+    int bi = 0x7fffffff;
+    for (uint32_t i = lo + threadIdx.x; i < hi; i += NTHR) argmax_merge(bv, bi, to_f(lr[i]), (int)i);
+    block_argmax<NTHR>(bv, bi);
+    if (threadIdx.x == 0) {
+        if (gridDim.x == 1) {
+            ids[row] = (bi == 0x7fffffff) ? 0 : bi;
+        } else {
+            pv[(size_t)row * gridDim.x + blockIdx.x] = bv;
+            pi[(size_t)row * gridDim.x + blockIdx.x] = bi;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float* pv, const int* pi,
+                                                           uint32_t nblk, int32_t* ids) {
+    const uint32_t row = blockIdx.x;
+    float bv = -FLT_MAX;
+    int bi = 0x7fffffff;
+    for (uint32_t i = threadIdx.x; i < nblk; i += 256)
+        argmax_merge(bv, bi, pv[(size_t)row * nblk + i], pi[(size_t)row * nblk + i]);
+    block_argmax<256>(bv, bi);
+    if (threadIdx.x == 0) ids[row] = (bi == 0x7fffffff) ? 0 : bi;
+}
+
+static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+hipError_t launch_rmsnorm(hipStream_t s, const void* x, uint32_t xs, const void* w, void* y,
+                          uint32_t ys, uint32_t rows, uint32_t dim, float eps, int act) {
+    if (rows == 0) return hipSuccess;
+    LSSM_DISPATCH_ACT(act, T,
+                      rmsnorm_kernel<T><<<rows, NT, 0, s>>>((const T*)x, xs, (const T*)w, (T*)y, ys,
+                                                            dim, eps));
+    return hipGetLastError();
+}
+
+hipError_t launch_gated_rmsnorm(hipStream_t s, const void* z, uint32_t zs, const void* y,
+                                uint32_t yst, const void* w, void* out, uint32_t rows, uint32_t dim,
+                                float eps, int act) {
+    if (rows == 0) return hipSuccess;
+    LSSM_DISPATCH_ACT(act, T,
+                      gated_rmsnorm_kernel<T><<<rows, NT, 0, s>>>((const T*)z, zs, (const T*)y, yst,
+                                                                  (const T*)w, (T*)out, dim, eps));
+    return hipGetLastError();
+}
+
+hipError_t launch_silu(hipStream_t s, const void* x, void* y, uint32_t n, int act) {
+    if (n == 0) return hipSuccess;
+    LSSM_DISPATCH_ACT(act, T, silu_kernel<T><<<cdiv(n, NT), NT, 0, s>>>((const T*)x, (T*)y, n));
+    return hipGetLastError();
+}
+
+hipError_t launch_add(hipStream_t s, void* y, const void* x, uint32_t n, int act) {
+    if (n == 0) return hipSuccess;
+    LSSM_DISPATCH_ACT(act, T, add_kernel<T><<<cdiv(n, NT), NT, 0, s>>>((T*)y, (const T*)x, n));
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_gated(hipStream_t s, const void* x, const void* g, void* y, uint32_t n,
+                             int act) {
+    if (n == 0) return hipSuccess;
+    LSSM_DISPATCH_ACT(act, T,
+                      silu_gated_kernel<T><<<cdiv(n, NT), NT, 0, s>>>((const T*)x, (const T*)g,
+                                                                      (T*)y, n));
+    return hipGetLastError();
+}
+
+hipError_t launch_split_silu(hipStream_t s, const void* xBC, void* x, void* B, void* C,
+                             uint32_t rows, uint32_t d_inner, uint32_t GN, int act) {
+    size_t n = (size_t)rows * (d_inner + 2u * GN);
+    if (n == 0) return hipSuccess;
+    LSSM_DISPATCH_ACT(act, T,
+                      split_silu_kernel<T><<<cdiv(n, NT), NT, 0, s>>>((const T*)xBC, (T*)x, (T*)B,
+                                                                      (T*)C, rows, d_inner, GN));
+    return hipGetLastError();
+}
+
+hipError_t launch_conv1d(hipStream_t s, const void* x, uint32_t xs, const void* w, const void* bias,
+                         void* y, uint32_t ys, uint32_t B, uint32_t L, uint32_t D, uint32_t K,
+                         int act, bool silu) {
+    if ((size_t)B * L * D == 0) return hipSuccess;
+    dim3 grid(cdiv(D, NT), L, B);
+    if (silu) {
+        LSSM_DISPATCH_ACT(act, T,
+                          conv1d_kernel<T, true><<<grid, NT, 0, s>>>((const T*)x, xs, (const T*)w,
+                                                                     (const T*)bias, (T*)y, ys, L,
+                                                                     D, K));
+    } else {
+        LSSM_DISPATCH_ACT(act, T,
+                          conv1d_kernel<T, false><<<grid, NT, 0, s>>>((const T*)x, xs, (const T*)w,
+                                                                      (const T*)bias, (T*)y, ys, L,
+                                                                      D, K));
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_conv1d_update(hipStream_t s, const void* x_new, void* state, const void* w,
+                                const void* bias, void* y, uint32_t B, uint32_t D, uint32_t K,
+                                int act) {
+    if ((size_t)B * D == 0) return hipSuccess;
+    dim3 grid(cdiv(D, NT), B);
+    LSSM_DISPATCH_ACT(act, T,
+                      conv1d_update_kernel<T><<<grid, NT, 0, s>>>((const T*)x_new, (T*)state,
+                                                                  (const T*)w, (const T*)bias,
+                                                                  (T*)y, D, K));
+    return hipGetLastError();
+}
+
+hipError_t launch_conv1d_seed(hipStream_t s, const void* xBC, uint32_t xs, void* state, uint32_t B,
+                              uint32_t L, uint32_t D, uint32_t K, int act) {
+    if ((size_t)B * D == 0) return hipSuccess;
+    dim3 grid(cdiv(D, NT), B);
+    LSSM_DISPATCH_ACT(act, T,
+                      conv1d_seed_kernel<T><<<grid, NT, 0, s>>>((const T*)xBC, xs, (T*)state, L, D,
+                                                                K));
+    return hipGetLastError();
+}
+
+hipError_t launch_conv1d_update_silu(hipStream_t s, const void* x_new, uint32_t xs, void* state,
+                                     const void* w, const void* bias, void* y, uint32_t ys,
+                                     uint32_t B, uint32_t D, uint32_t K, int act) {
+    if ((size_t)B * D == 0) return hipSuccess;
+    dim3 grid(cdiv(D, NT), B);
+    LSSM_DISPATCH_ACT(act, T,
+                      conv1d_update_silu_kernel<T><<<grid, NT, 0, s>>>((const T*)x_new, xs, (T*)state,
+                                                                       (const T*)w, (const T*)bias,
+                                                                       (T*)y, ys, D, K));
+    return hipGetLastError();
+}
+
+hipError_t launch_conv1d_keep_last(hipStream_t s, void* state, uint32_t n_windows, uint32_t K,
+                                   int act) {
+    const size_t n = (size_t)n_windows * (K - 1);
+    if (n == 0) return hipSuccess;
+    LSSM_DISPATCH_ACT(act, T,
+                      conv1d_keep_last_kernel<T><<<cdiv(n, NT), NT, 0, s>>>((T*)state, n_windows, K));
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, void* out, uint32_t n,
+                        uint32_t d_model, uint32_t vocab, int act) {
+    if (n == 0) return hipSuccess;
+    dim3 grid(cdiv(d_model, NT), n);
+    LSSM_DISPATCH_ACT(act, T,
+                      embed_kernel<T><<<grid, NT, 0, s>>>((const T*)table, ids, (T*)out, d_model,
+                                                          vocab));
+    return hipGetLastError();
+}
+
+// scratch == nullptr: single pass, one 1024-thread block per row.
+// scratch != nullptr: 128 blocks per row, then a final pass; scratch must hold
+// rows * 128 * (sizeof(float) + sizeof(int)) bytes.
+hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32_t rows,
+                         uint32_t vocab, int act, void* scratch) {
+    if (rows == 0) return hipSuccess;
+    if (!scratch) {
+        LSSM_DISPATCH_ACT(act, T,
+                          argmax_partial_kernel<T, 1024><<<dim3(1, rows), 1024, 0, s>>>(
+                              (const T*)logits, vocab, nullptr, nullptr, ids));
+        return hipGetLastError();
+    }
+    const uint32_t nblk = 128;
+    float* pv = (float*)scratch;
+    int* pi = (int*)(pv + (size_t)rows * nblk);
+    LSSM_DISPATCH_ACT(act, T,
+                      argmax_partial_kernel<T, 256><<<dim3(nblk, rows), 256, 0, s>>>(
+                          (const T*)logits, vocab, pv, pi, ids));
+    argmax_final_kernel<<<rows, 256, 0, s>>>(pv, pi, nblk, ids);
+    return hipGetLastError();
+}
+
+}  // namespace lssm

@@ -1,0 +1,444 @@
+// engine.hip — whole-model Mamba-2 prefill / decode on one GPU.
+//
+// Runs the op sequence of Mamba2Model::run_block (mamba2_block.cpp:51-290),
+// forward_prefill / forward_step (:296-327) and compute_logits
+// (mamba2_model.cpp:144-175), generalised to a batch of sequences, with:
+//   - decode fused to 3 kernels per layer for batch <= 4:
+//       [RMSNorm + in_proj GEMV + conv update + SiLU split]
+//       [SSD step + SiLU(z) gate]
+//       [gated RMSNorm + out_proj GEMV + residual add]
+//     (batch > 4 runs the MFMA GEMM with separate norm / conv kernels);
+//   - prefill on the MFMA GEMM and the MFMA chunked scan;
+//   - embedding gather and greedy argmax on the device, so a decode step has
+//     no host round trip and can be captured once into a HIP graph.
+// Every intermediate is rounded at the same points as the reference's
+// unfused kernels.
+#include <vector>
+
+#include "internal.hpp"
+
+using namespace lssm;
+
+namespace {
+constexpr float RMS_EPS = 1e-5f;   // mamba2_block.cpp:45
+constexpr float DT_MIN = 1e-6f;    // mamba2_block.cpp:43
+constexpr float DT_MAX = 1e6f;     // mamba2_block.cpp:44
+}  // namespace
+
+struct lssm_engine {
+    lssm_ctx* ctx = nullptr;
+    lssm_model_config cfg{};
+    uint32_t d_model = 0, d_inner = 0, xbc = 0, proj = 0, H = 0, P = 0, N = 0, G = 0, K = 0,
+             vocab = 0, GN = 0;
+    int act = 0, wfmt = 0;
+    size_t es = 2;
+    const void* embed = nullptr;
+    const void* norm_f = nullptr;
+    const void* lm_head = nullptr;
+    std::vector<lssm_layer_weights> layers;
+    uint32_t max_batch = 0, max_seq = 0;
+
+    std::vector<void*> allocs;
+    // prefill buffers [max_batch * max_seq, ...]
+    void* hidden = nullptr;
+    void* normed = nullptr;
+    void* projb = nullptr;
+    void* xbc_act = nullptr;
+    void* ys = nullptr;
+    void* gn = nullptr;
+    // decode buffers [max_batch, ...]
+    void* d_hidden = nullptr;
+    void* d_normed = nullptr;
+    void* d_proj = nullptr;
+    void* d_z = nullptr;
+    void* d_xbc = nullptr;
+    void* d_dt = nullptr;
+    void* d_g = nullptr;
+    void* d_gn = nullptr;
+    void* logits = nullptr;
+    void* conv_state = nullptr;
+    float* ssd_state = nullptr;
+    void* argmax_scratch = nullptr;
+
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    const int32_t* g_ids = nullptr;
+    int32_t* g_next = nullptr;
+    uint32_t g_batch = 0;
+
+    ~lssm_engine() {
+        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        for (void* p : allocs) (void)hipFree(p);
+    }
+
+    int alloc(void** p, size_t n) {
+        if (n == 0) n = 16;
+        hipError_t e = hipMalloc(p, n);
+        if (e != hipSuccess) return set_error(LSSM_EDEVICE, "engine: hipMalloc(%zu): %s", n, hipGetErrorString(e));
+        allocs.push_back(*p);
+        return LSSM_OK;
+    }
+
+    char* conv_layer(uint32_t li) const {
+        return (char*)conv_state + (size_t)li * max_batch * xbc * K * es;
+    }
+    float* ssd_layer(uint32_t li) const { return ssd_state + (size_t)li * max_batch * H * P * N; }
+
+    hipStream_t st() const { return ctx->stream; }
+
+    // Linear on the fastest kernel for the shape (GEMV for M <= 4).
+    hipError_t linear(const void* x, uint32_t xs, const void* w, const void* s, void* y, uint32_t ysd,
+                      const void* res, uint32_t M, uint32_t Nn, uint32_t Kk, int fmt, int epi) const {
+        if (M <= 4) {
+            GemvArgs g{x, xs, w, s, y, ysd, res, nullptr, 0.0f, M, Nn, Kk, fmt, act, epi};
+            return launch_gemv(st(), g);
+        }
+        GemmArgs g{x, xs, w, s, y, ysd, res, M, Nn, Kk, fmt, act, epi, 1};
+        if (act == LSSM_F32) return launch_gemm_simple(st(), g);
+        return launch_gemm(st(), g);
+    }
+
+    // Logits of `rows` hidden rows (row stride xs) -> logits, then argmax.
+    hipError_t logits_argmax(const void* x, uint32_t xs, uint32_t rows, int32_t* next) const {
+        hipError_t e;
+        if (rows <= 4 && (size_t)rows * d_model * 4 <= 64 * 1024) {
+            GemvArgs g{x, xs, lm_head, nullptr, logits, vocab, nullptr, norm_f, RMS_EPS, rows, vocab,
+                       d_model, LSSM_W_DENSE, act, LSSM_EPI_NONE};
+            e = launch_gemv(st(), g);
+        } else {
+            e = launch_rmsnorm(st(), x, xs, norm_f, d_normed, d_model, rows, d_model, RMS_EPS, act);
+            if (e == hipSuccess)
+                e = linear(d_normed, d_model, lm_head, nullptr, logits, vocab, nullptr, rows, vocab,
+                           d_model, LSSM_W_DENSE, LSSM_EPI_NONE);
+        }
+        if (e == hipSuccess) e = launch_argmax(st(), logits, next, rows, vocab, act, argmax_scratch);
+        return e;
+    }
+
+    // One decode step: ids -> next (all on device).  mamba2_block.cpp:317-327.
+    hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
+        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act);
+        const bool fused_in = (size_t)B * d_model * 4 <= 64 * 1024 && B <= 4;
+        const bool fused_out = (size_t)B * d_inner * 4 <= 64 * 1024 && B <= 4;
+        for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
+            const lssm_layer_weights& w = layers[li];
+            char* cs = conv_layer(li);
+            if (fused_in) {
+                InprojDecodeArgs a;
+                a.g = GemvArgs{d_hidden, d_model, w.in_proj_w, w.in_proj_s, nullptr, 0, nullptr,
+                               w.norm_w, RMS_EPS, B, proj, d_model, wfmt, act, LSSM_EPI_NONE};
+                a.d_inner = d_inner;
+                a.xbc = xbc;
+                a.H = H;
+                a.dconv = K;
+                a.conv_state = cs;
+                a.conv_w = w.conv1d_w;
+                a.conv_b = w.conv1d_b;
+                a.z = d_z;
+                a.xbc_act = d_xbc;
+                a.dt = d_dt;
+                e = launch_inproj_decode(st(), a);
+            } else {
+                e = launch_rmsnorm(st(), d_hidden, d_model, w.norm_w, d_normed, d_model, B, d_model,
+                                   RMS_EPS, act);
+                if (e == hipSuccess)
+                    e = linear(d_normed, d_model, w.in_proj_w, w.in_proj_s, d_proj, proj, nullptr, B,
+                               proj, d_model, wfmt, LSSM_EPI_NONE);
+                if (e == hipSuccess)
+                    e = launch_conv1d_update_silu(st(), (char*)d_proj + (size_t)d_inner * es, proj, cs,
+                                                  w.conv1d_w, w.conv1d_b, d_xbc, xbc, B, xbc, K, act);
+            }
+            if (e != hipSuccess) break;
+            // z / dt live in d_z, d_dt (fused) or inside d_proj (strided)
+            const void* z = fused_in ? d_z : d_proj;
+            const uint32_t zs = fused_in ? d_inner : proj;
+            const void* dt = fused_in ? d_dt : (const void*)((char*)d_proj + (size_t)(d_inner + xbc) * es);
+            const uint32_t dts = fused_in ? H : proj;
+            SsdArgs s{d_xbc, xbc, (char*)d_xbc + (size_t)d_inner * es, xbc,
+                      (char*)d_xbc + (size_t)(d_inner + GN) * es, xbc, dt, dts, w.dt_bias, w.A_log,
+                      w.D, d_g, d_inner, ssd_layer(li), B, 1, H, P, N, G, 1, DT_MIN, DT_MAX, 1u, act,
+                      z, zs};
+            e = launch_ssd_step(st(), s);
+            if (e != hipSuccess) break;
+            if (fused_out) {
+                GemvArgs g{d_g, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden,
+                           w.mixer_norm_w, RMS_EPS, B, d_model, d_inner, wfmt, act, LSSM_EPI_ADD};
+                e = launch_gemv(st(), g);
+            } else {
+                e = launch_rmsnorm(st(), d_g, d_inner, w.mixer_norm_w, d_gn, d_inner, B, d_inner,
+                                   RMS_EPS, act);
+                if (e == hipSuccess)
+                    e = linear(d_gn, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden,
+                               B, d_model, d_inner, wfmt, LSSM_EPI_ADD);
+            }
+        }
+        if (e == hipSuccess) e = logits_argmax(d_hidden, d_model, B, next);
+        return e;
+    }
+
+    // Prefill of B sequences of L tokens (mamba2_block.cpp:296-315).  L == 1
+    // follows the reference's 1-token path (GEMV, conv update, SSD step, then
+    // the state seed).
+    hipError_t prefill(const int32_t* ids, uint32_t B, uint32_t L, int32_t* next) const {
+        if (L == 1) {
+            hipError_t e = decode_layers_for_prefill1(ids, B);
+            if (e == hipSuccess) e = logits_argmax(d_hidden, d_model, B, next);
+            return e;
+        }
+        const uint32_t R = B * L;
+        hipError_t e = launch_embed(st(), embed, ids, hidden, R, d_model, vocab, act);
+        const uint32_t ck = cfg.chunk_size < L ? (cfg.chunk_size < 64 ? cfg.chunk_size : 64)
+                                               : (L < 64 ? L : 64);
+        for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
+            const lssm_layer_weights& w = layers[li];
+            e = launch_rmsnorm(st(), hidden, d_model, w.norm_w, normed, d_model, R, d_model, RMS_EPS, act);
+            if (e == hipSuccess) {
+                GemmArgs g{normed, d_model, w.in_proj_w, w.in_proj_s, projb, proj, nullptr, R, proj,
+                           d_model, wfmt, act, LSSM_EPI_NONE, 1};
+                e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
+            }
+            const char* xbc_pre = (const char*)projb + (size_t)d_inner * es;
+            if (e == hipSuccess)
+                e = launch_conv1d(st(), xbc_pre, proj, w.conv1d_w, w.conv1d_b, xbc_act, xbc, B, L, xbc,
+                                  K, act, true);
+            if (e == hipSuccess) e = launch_conv1d_seed(st(), xbc_pre, proj, conv_layer(li), B, L, xbc, K, act);
+            if (e == hipSuccess) {
+                SsdArgs s{xbc_act, xbc, (char*)xbc_act + (size_t)d_inner * es, xbc,
+                          (char*)xbc_act + (size_t)(d_inner + GN) * es, xbc,
+                          (char*)projb + (size_t)(d_inner + xbc) * es, proj, w.dt_bias, w.A_log, w.D,
+                          ys, d_inner, ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act,
+                          nullptr, 0};
+                e = launch_ssd_chunked(st(), s);
+            }
+            if (e == hipSuccess)
+                e = launch_gated_rmsnorm(st(), projb, proj, ys, d_inner, w.mixer_norm_w, gn, R, d_inner,
+                                         RMS_EPS, act);
+            if (e == hipSuccess) {
+                GemmArgs g{gn, d_inner, w.out_proj_w, w.out_proj_s, hidden, d_model, hidden, R, d_model,
+                           d_inner, wfmt, act, LSSM_EPI_ADD, 1};
+                e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
+            }
+        }
+        // last position of each sequence: rows (b*L + L-1), stride L*d_model
+        if (e == hipSuccess)
+            e = logits_argmax((const char*)hidden + (size_t)(L - 1) * d_model * es, L * d_model, B, next);
+        return e;
+    }
+
+    hipError_t decode_layers_for_prefill1(const int32_t* ids, uint32_t B) const {
+        // same kernels as a decode step without logits, then the 1-row seed
+        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act);
+        for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
+            const lssm_layer_weights& w = layers[li];
+            e = launch_rmsnorm(st(), d_hidden, d_model, w.norm_w, d_normed, d_model, B, d_model, RMS_EPS, act);
+            if (e == hipSuccess)
+                e = linear(d_normed, d_model, w.in_proj_w, w.in_proj_s, d_proj, proj, nullptr, B, proj,
+                           d_model, wfmt, LSSM_EPI_NONE);
+            if (e == hipSuccess)
+                e = launch_conv1d_update_silu(st(), (char*)d_proj + (size_t)d_inner * es, proj,
+                                              conv_layer(li), w.conv1d_w, w.conv1d_b, d_xbc, xbc, B,
+                                              xbc, K, act);
+            if (e == hipSuccess) e = launch_conv1d_keep_last(st(), conv_layer(li), B * xbc, K, act);
+            if (e != hipSuccess) break;
+            SsdArgs s{d_xbc, xbc, (char*)d_xbc + (size_t)d_inner * es, xbc,
+                      (char*)d_xbc + (size_t)(d_inner + GN) * es, xbc,
+                      (char*)d_proj + (size_t)(d_inner + xbc) * es, proj, w.dt_bias, w.A_log, w.D,
+                      d_g, d_inner, ssd_layer(li), B, 1, H, P, N, G, 1, DT_MIN, DT_MAX, 1u, act,
+                      d_proj, proj};
+            e = launch_ssd_step(st(), s);
+            if (e == hipSuccess)
+                e = launch_rmsnorm(st(), d_g, d_inner, w.mixer_norm_w, d_gn, d_inner, B, d_inner, RMS_EPS, act);
+            if (e == hipSuccess)
+                e = linear(d_gn, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden, B,
+                           d_model, d_inner, wfmt, LSSM_EPI_ADD);
+        }
+        return e;
+    }
+};
+
+namespace {
+
+int check_engine(lssm_engine* e) {
+    if (!e) return set_error(LSSM_EINVAL, "null lssm_engine");
+    clear_error();
+    return LSSM_OK;
+}
+
+int engine_finish(lssm_engine* e, hipError_t err, const char* what) {
+    if (err != hipSuccess) return set_error(LSSM_EDEVICE, "%s: %s", what, hipGetErrorString(err));
+    return finish(e->ctx, what);
+}
+
+}  // namespace
+
+extern "C" {
+
+int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config* cfg,
+                       const void* embed, const void* norm_f, const void* lm_head,
+                       const lssm_layer_weights* layers, uint32_t max_batch, uint32_t max_seq) {
+    LSSM_CHECK_CTX(ctx);
+    LSSM_REQUIRE(out && cfg && embed && norm_f && layers, "engine_create: null argument");
+    LSSM_REQUIRE(valid_act((int)cfg->act), "engine_create: unknown activation dtype");
+    LSSM_REQUIRE(valid_wfmt((int)cfg->wfmt), "engine_create: unknown weight format");
+    LSSM_REQUIRE(cfg->n_layer > 0 && cfg->d_model > 0 && cfg->expand > 0 && cfg->d_state > 0 &&
+                     cfg->d_conv > 0 && cfg->n_heads > 0 && cfg->d_head > 0 && cfg->vocab_size > 0,
+                 "engine_create: zero dimension in config");
+    const uint32_t G = cfg->n_groups ? cfg->n_groups : 1;
+    const uint32_t d_inner = cfg->expand * cfg->d_model;
+    LSSM_REQUIRE(cfg->n_heads * cfg->d_head == d_inner, "engine_create: n_heads * d_head != d_inner");
+    LSSM_REQUIRE(cfg->n_heads % G == 0, "engine_create: n_heads must be a multiple of n_groups");
+    LSSM_REQUIRE(max_batch >= 1 && max_seq >= 1, "engine_create: max_batch and max_seq must be >= 1");
+    if (cfg->wfmt != LSSM_W_DENSE) {
+        const uint32_t g = wfmt_group((int)cfg->wfmt);
+        LSSM_REQUIRE(cfg->d_model % g == 0 && d_inner % g == 0,
+                     "engine_create: d_model and d_inner must be multiples of the group size");
+    }
+    LSSM_REQUIRE(cfg->d_model % 64 == 0 && d_inner % 64 == 0,
+                 "engine_create: d_model and d_inner must be multiples of 64");
+    LSSM_REQUIRE(cfg->d_model <= 16384 && d_inner <= 16384, "engine_create: d_model/d_inner > 16384");
+    LSSM_REQUIRE(cfg->chunk_size >= 1, "engine_create: chunk_size must be >= 1");
+
+    auto* e = new lssm_engine();
+    e->ctx = ctx;
+    e->cfg = *cfg;
+    e->cfg.n_groups = G;
+    e->act = (int)cfg->act;
+    e->wfmt = (int)cfg->wfmt;
+    e->es = dtype_size(e->act);
+    e->d_model = cfg->d_model;
+    e->d_inner = d_inner;
+    e->G = G;
+    e->N = cfg->d_state;
+    e->GN = G * cfg->d_state;
+    e->xbc = d_inner + 2 * e->GN;
+    e->H = cfg->n_heads;
+    e->P = cfg->d_head;
+    e->proj = d_inner + e->xbc + e->H;
+    e->K = cfg->d_conv;
+    e->vocab = cfg->vocab_size;
+    e->embed = embed;
+    e->norm_f = norm_f;
+    e->lm_head = lm_head ? lm_head : embed;   // tied lm_head (mamba2_model.cpp:75-83)
+    e->layers.assign(layers, layers + cfg->n_layer);
+    e->max_batch = max_batch;
+    e->max_seq = max_seq;
+
+    const size_t es = e->es;
+    const size_t R = (size_t)max_batch * max_seq;
+    int rc = LSSM_OK;
+    auto A = [&](void** p, size_t n) {
+        if (rc == LSSM_OK) rc = e->alloc(p, n);
+    };
+    A(&e->hidden, R * e->d_model * es);
+    A(&e->normed, R * e->d_model * es);
+    A(&e->projb, R * e->proj * es);
+    A(&e->xbc_act, R * e->xbc * es);
+    A(&e->ys, R * d_inner * es);
+    A(&e->gn, R * d_inner * es);
+    A(&e->d_hidden, (size_t)max_batch * e->d_model * es);
+    A(&e->d_normed, (size_t)max_batch * e->d_model * es);
+    A(&e->d_proj, (size_t)max_batch * e->proj * es);
+    A(&e->d_z, (size_t)max_batch * d_inner * es);
+    A(&e->d_xbc, (size_t)max_batch * e->xbc * es);
+    A(&e->d_dt, (size_t)max_batch * e->H * es);
+    A(&e->d_g, (size_t)max_batch * d_inner * es);
+    A(&e->d_gn, (size_t)max_batch * d_inner * es);
+    A(&e->logits, (size_t)max_batch * e->vocab * es);
+    A(&e->conv_state, (size_t)cfg->n_layer * max_batch * e->xbc * e->K * es);
+    A((void**)&e->ssd_state, (size_t)cfg->n_layer * max_batch * e->H * e->P * e->N * sizeof(float));
+    A(&e->argmax_scratch, (size_t)max_batch * 128 * 8);
+    if (rc != LSSM_OK) {
+        delete e;
+        return rc;
+    }
+    *out = e;
+    return lssm_engine_reset(e);
+}
+
+int lssm_engine_destroy(lssm_engine* e) {
+    clear_error();
+    if (!e) return LSSM_OK;
+    (void)hipStreamSynchronize(e->ctx->stream);
+    delete e;
+    return LSSM_OK;
+}
+
+int lssm_engine_reset(lssm_engine* e) {
+    if (int rc = check_engine(e)) return rc;
+    hipError_t err = hipMemsetAsync(e->conv_state, 0,
+                                    (size_t)e->cfg.n_layer * e->max_batch * e->xbc * e->K * e->es,
+                                    e->ctx->stream);
+    if (err == hipSuccess)
+        err = hipMemsetAsync(e->ssd_state, 0,
+                             (size_t)e->cfg.n_layer * e->max_batch * e->H * e->P * e->N * sizeof(float),
+                             e->ctx->stream);
+    return engine_finish(e, err, "engine_reset");
+}
+
+int lssm_engine_prefill(lssm_engine* e, const int32_t* ids, uint32_t batch, uint32_t L,
+                        int32_t* next_ids) {
+    if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(L >= 1, "forward_prefill: L must be >= 1");                       // mamba2_block.cpp:300
+    LSSM_REQUIRE(L <= e->max_seq, "forward_prefill: L exceeds workspace max_seq_len"); // :301-303
+    LSSM_REQUIRE(batch >= 1 && batch <= e->max_batch, "forward_prefill: batch out of range");
+    LSSM_REQUIRE(ids && next_ids, "forward_prefill: null ids");
+    return engine_finish(e, e->prefill(ids, batch, L, next_ids), "engine_prefill");
+}
+
+int lssm_engine_decode(lssm_engine* e, const int32_t* ids, uint32_t batch, int32_t* next_ids) {
+    if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(batch >= 1 && batch <= e->max_batch, "forward_step: batch out of range");
+    LSSM_REQUIRE(ids && next_ids, "forward_step: null ids");
+    return engine_finish(e, e->decode(ids, batch, next_ids), "engine_decode");
+}
+
+int lssm_engine_decode_graph(lssm_engine* e, const int32_t* ids, uint32_t batch, int32_t* next_ids,
+                             uint32_t steps) {
+    if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(batch >= 1 && batch <= e->max_batch, "forward_step: batch out of range");
+    LSSM_REQUIRE(ids && next_ids, "forward_step: null ids");
+    hipStream_t s = e->ctx->stream;
+    if (!e->graph_exec || e->g_ids != ids || e->g_next != next_ids || e->g_batch != batch) {
+        if (e->graph_exec) {
+            (void)hipGraphExecDestroy(e->graph_exec);
+            e->graph_exec = nullptr;
+        }
+        if (e->graph) {
+            (void)hipGraphDestroy(e->graph);
+            e->graph = nullptr;
+        }
+        hipError_t err = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: begin capture");
+        hipError_t le = e->decode(ids, batch, next_ids);
+        err = hipStreamEndCapture(s, &e->graph);
+        if (le != hipSuccess) return engine_finish(e, le, "engine_decode_graph: capture");
+        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: end capture");
+        err = hipGraphInstantiate(&e->graph_exec, e->graph, nullptr, nullptr, 0);
+        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: instantiate");
+        e->g_ids = ids;
+        e->g_next = next_ids;
+        e->g_batch = batch;
+    }
+    for (uint32_t i = 0; i < steps; ++i) {
+        hipError_t err = hipGraphLaunch(e->graph_exec, s);
+        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: launch");
+    }
+    return finish(e->ctx, "engine_decode_graph");
+}
+
+int lssm_engine_logits(lssm_engine* e, void** logits) {
+    if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(logits, "engine_logits: null out");
+    *logits = e->logits;
+    return LSSM_OK;
+}
+
+int lssm_engine_state(lssm_engine* e, void** conv_state, void** ssd_state) {
+    if (int rc = check_engine(e)) return rc;
+    if (conv_state) *conv_state = e->conv_state;
+    if (ssd_state) *ssd_state = e->ssd_state;
+    return LSSM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,163 @@
+// internal.hpp — host-side plumbing shared by the C-ABI translation units.
+//
+// The C entry points validate arguments on the host (so a bad shape becomes an
+// LSSM_EINVAL, never an out-of-bounds kernel), launch on the context's stream,
+// and then either return (inside a batch) or synchronise and check (outside),
+// matching MetalOps' batched / one-shot split (ops.mm:82-149).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/lssm.h"
+
+struct lssm_ctx {
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    bool batch = false;
+    int device = 0;
+};
+
+namespace lssm {
+
+// thread-local error message (lssm_last_error)
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+
+// After enqueueing an op: report launch errors; outside a batch, also wait and
+// report asynchronous kernel failures.
+int finish(lssm_ctx* ctx, const char* what);
+
+inline size_t dtype_size(int act) { return act == LSSM_F32 ? 4 : 2; }
+inline bool valid_act(int act) { return act == LSSM_F16 || act == LSSM_BF16 || act == LSSM_F32; }
+inline bool valid_wfmt(int f) {
+    return f == LSSM_W_DENSE || f == LSSM_W_Q4_B32 || f == LSSM_W_Q4_G64 || f == LSSM_W_Q8_G32;
+}
+inline uint32_t wfmt_group(int f) {
+    return f == LSSM_W_Q4_G64 ? 64u : (f == LSSM_W_DENSE ? 0u : 32u);
+}
+
+#define LSSM_CHECK_CTX(ctx)                                                 \
+    do {                                                                    \
+        if (!(ctx)) return ::lssm::set_error(LSSM_EINVAL, "null lssm_ctx"); \
+        ::lssm::clear_error();                                              \
+    } while (0)
+
+#define LSSM_REQUIRE(cond, ...)                                             \
+    do {                                                                    \
+        if (!(cond)) return ::lssm::set_error(LSSM_EINVAL, __VA_ARGS__);    \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Launchers (defined in the .hip files).  All return hipError_t of the launch.
+// Row strides are in elements.
+// ---------------------------------------------------------------------------
+hipError_t launch_rmsnorm(hipStream_t s, const void* x, uint32_t x_stride, const void* w, void* y,
+                          uint32_t y_stride, uint32_t rows, uint32_t dim, float eps, int act);
+hipError_t launch_gated_rmsnorm(hipStream_t s, const void* z, uint32_t z_stride, const void* y,
+                                uint32_t y_stride, const void* w, void* out, uint32_t rows,
+                                uint32_t dim, float eps, int act);
+hipError_t launch_silu(hipStream_t s, const void* x, void* y, uint32_t n, int act);
+hipError_t launch_add(hipStream_t s, void* y, const void* x, uint32_t n, int act);
+hipError_t launch_silu_gated(hipStream_t s, const void* x, const void* g, void* y, uint32_t n,
+                             int act);
+hipError_t launch_split_silu(hipStream_t s, const void* xBC, void* x, void* B, void* C,
+                             uint32_t rows, uint32_t d_inner, uint32_t GN, int act);
+hipError_t launch_conv1d(hipStream_t s, const void* x, uint32_t x_stride, const void* w,
+                         const void* bias, void* y, uint32_t y_stride, uint32_t B, uint32_t L,
+                         uint32_t D, uint32_t K, int act, bool silu);
+hipError_t launch_conv1d_update(hipStream_t s, const void* x_new, void* state, const void* w,
+                                const void* bias, void* y, uint32_t B, uint32_t D, uint32_t K,
+                                int act);
+hipError_t launch_conv1d_update_silu(hipStream_t s, const void* x_new, uint32_t x_stride,
+                                     void* state, const void* w, const void* bias, void* y,
+                                     uint32_t y_stride, uint32_t B, uint32_t D, uint32_t K, int act);
+hipError_t launch_conv1d_keep_last(hipStream_t s, void* state, uint32_t n_windows, uint32_t K,
+                                   int act);
+hipError_t launch_conv1d_seed(hipStream_t s, const void* xBC, uint32_t x_stride, void* state,
+                              uint32_t B, uint32_t L, uint32_t D, uint32_t K, int act);
+hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, void* out,
+                        uint32_t n, uint32_t d_model, uint32_t vocab, int act);
+hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32_t rows,
+                         uint32_t vocab, int act, void* scratch);
+
+// GEMV (M <= 4): optional RMSNorm prologue over each x row (norm_w != nullptr).
+struct GemvArgs {
+    const void* x;
+    uint32_t x_stride;
+    const void* w;
+    const void* s;
+    void* y;
+    uint32_t y_stride;
+    const void* res;
+    const void* norm_w;
+    float eps;
+    uint32_t M, N, K;
+    int wfmt, act, epi;
+};
+hipError_t launch_gemv(hipStream_t s, const GemvArgs& a);
+hipError_t launch_dequant(hipStream_t s, const void* w, const void* sc, float* out, uint32_t N,
+                          uint32_t K, int wfmt);
+
+// MFMA GEMM for fp16 / bf16 activations, K % 64 == 0.
+struct GemmArgs {
+    const void* x;
+    uint32_t x_stride;
+    const void* w;
+    const void* s;
+    void* y;
+    uint32_t y_stride;
+    const void* res;
+    uint32_t M, N, K;
+    int wfmt, act, epi;
+    int round_dequant;   // gemm_simple only: 1 = GEMM semantics, 0 = exact (GEMV)
+};
+hipError_t launch_gemm(hipStream_t s, const GemmArgs& a);
+// Simple fp32 (or any dtype) reference-layout GEMM used for F32 activations.
+hipError_t launch_gemm_simple(hipStream_t s, const GemmArgs& a);
+
+// SSD.  Strides are row strides in elements of the [.., L, ...] tensors.
+struct SsdArgs {
+    const void* X;  uint32_t x_stride;   // row = one token: H*P elements (packed)
+    const void* B;  uint32_t b_stride;   // row = one token: G*N
+    const void* C;  uint32_t c_stride;
+    const void* dt; uint32_t dt_stride;  // row = one token: H
+    const void* dt_bias;
+    const void* A_log;
+    const void* D;
+    void* Y;        uint32_t y_stride;
+    float* state;
+    uint32_t batch, L, H, P, N, G, chunk;
+    float dt_min, dt_max;
+    uint32_t has_D;
+    int act;
+    // optional gate (decode engine): Y = r(silu(z) * r(y)); z row stride
+    const void* z;  uint32_t z_stride;
+};
+hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a);
+hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a);
+
+hipError_t launch_inproj_fused(hipStream_t s, const void* normed, const void* W_in,
+                               const void* W_conv, const void* conv_b, void* proj_z, void* ssd_x,
+                               void* ssd_B, void* ssd_C, void* proj_dt, void* proj_xBC,
+                               lssm_fused_inproj_dims d);
+
+// Engine decode in_proj: GEMV with RMSNorm prologue whose epilogue routes rows
+// to z / (conv update + SiLU -> xbc_act) / dt.
+struct InprojDecodeArgs {
+    GemvArgs g;           // y unused; res unused
+    uint32_t d_inner, xbc, H, dconv;
+    void* conv_state;     // [B, xbc, dconv] for this layer
+    const void* conv_w;   // [xbc, dconv]
+    const void* conv_b;   // [xbc]
+    void* z;              // [B, d_inner]
+    void* xbc_act;        // [B, xbc]
+    void* dt;             // [B, H]
+};
+hipError_t launch_inproj_decode(hipStream_t s, const InprojDecodeArgs& a);
+
+}  // namespace lssm

@@ -1,0 +1,34 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
+
+
+@pytest.fixture(scope="session")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+@pytest.fixture(scope="session")
+def ctx(torch_cuda):
+    import lite_ssm_amd as L
+    c = L.Ctx(stream=torch_cuda.cuda.current_stream().cuda_stream)
+    yield c
+    c.close()
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(1234)

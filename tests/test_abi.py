@@ -1,0 +1,78 @@
+"""The C-ABI library loads and exports every entry point include/lssm.h declares
+(no GPU needed; no compute calls)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# The 19 kernel entry points of the reference's shaders/*.metal
+# (tests/test_metal_ops.cpp:31-49 lists 17; the model also calls
+# split_silu_xBC_f16 and add_inplace_f16).
+REFERENCE_KERNELS = [
+    "lite_ssm_common_noop", "rmsnorm_f16", "linear_f16_gemv", "linear_silu_f16_gemv",
+    "rmsnorm_linear_f16_gemv", "linear_f16_gemm", "linear_silu_f16_gemm", "linear_int4_gemv",
+    "linear_int4_gemm", "silu_f16", "add_inplace_f16", "split_silu_xBC_f16", "silu_gated_f16",
+    "causal_conv1d_f16", "causal_conv1d_update_f16", "seed_conv_state_f16", "inproj_fused_f16",
+    "ssd_chunked_f16", "ssd_step_f16",
+]
+
+
+def header_symbols():
+    txt = open(os.path.join(ROOT, "include", "lssm.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(lssm_[a-zA-Z0-9_]+)\s*\(", txt)))
+
+
+def test_header_declares_reference_dispatchers():
+    syms = set(header_symbols())
+    # one entry per MetalOps dispatcher (include/lite_ssm/ops.hpp:99-235)
+    for k in REFERENCE_KERNELS[1:]:
+        assert "lssm_" + k in syms, k
+
+
+def test_library_exports_every_declared_symbol():
+    import lite_ssm_amd as L
+    lib = C.CDLL(L.LIB_PATH)
+    missing = [s for s in header_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    assert sorted(L.exported_symbols()) == header_symbols()
+
+
+def test_kernel_registry_answers_reference_names():
+    import lite_ssm_amd as L
+    for k in REFERENCE_KERNELS:
+        assert L.lib.lssm_has_kernel(k.encode()) == 1, k
+    assert L.lib.lssm_has_kernel(b"no_such_kernel") == 0
+    names = [L.lib.lssm_kernel_name(i).decode() for i in range(L.lib.lssm_kernel_count())]
+    assert set(REFERENCE_KERNELS) <= set(names)
+    assert os.path.samefile(L.lib.lssm_library_path().decode(), L.LIB_PATH)
+
+
+def test_null_context_is_an_error_not_a_crash():
+    import lite_ssm_amd as L
+    d = L.LinearDims(1, 8, 32)
+    rc = L.lib.lssm_linear_int4_gemv(None, None, None, None, None, d)
+    assert rc == 1
+    assert "null lssm_ctx" in L.lib.lssm_last_error().decode()
+    assert L.lib.lssm_batch_active(None) == 0
+    with pytest.raises(L.LssmError):
+        L.check(L.lib.lssm_sync(None))
+
+
+def test_engine_null_handle_is_an_error():
+    import lite_ssm_amd as L
+    assert L.lib.lssm_engine_decode(None, None, 1, None) == 1
+    assert "null lssm_engine" in L.lib.lssm_last_error().decode()
+
+
+def test_oracle_library_is_separate_from_product():
+    """The product library must not link the oracle."""
+    import lite_ssm_amd as L
+    import subprocess
+    out = subprocess.run(["ldd", L.LIB_PATH], capture_output=True, text=True).stdout
+    assert "oracle" not in out
+    data = open(L.LIB_PATH, "rb").read()
+    assert b"orc_model_decode" not in data
