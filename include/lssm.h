@@ -250,6 +250,21 @@ int lssm_ssd_step(lssm_ctx* ctx, const void* x, const void* B, const void* C,
                   const void* D_skip, float* state, void* y, uint32_t batch,
                   lssm_ssd_step_dims dims, lssm_dtype act);
 
+/* Fused decode in_proj for batch <= 4 rows (the engine's first kernel of a
+ * layer): normed = r(RMSNorm(hidden, norm_w)); proj = r(normed . deq(W)^T) over
+ * all [z | xBC | dt] rows; z and dt rows are stored, each xBC row goes through
+ * the conv-window update (conv1d.metal:108-137) and r(SiLU(r(conv))) into
+ * xbc_act.  Same arithmetic as rmsnorm_f16 -> 3 x linear gemv ->
+ * causal_conv1d_update_f16 -> split_silu_xBC_f16 (mamba2_block.cpp:84-177).
+ * conv_state [batch, xBC_dim, d_conv]; z [batch, d_inner];
+ * xbc_act [batch, xBC_dim]; dt [batch, n_heads]. */
+int lssm_inproj_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, const void* w,
+                       const void* w_scales, void* conv_state, const void* conv_w,
+                       const void* conv_b, void* z, void* xbc_act, void* dt, uint32_t batch,
+                       uint32_t d_model, uint32_t d_inner, uint32_t d_state, uint32_t n_groups,
+                       uint32_t n_heads, uint32_t d_conv, float eps, lssm_wfmt wfmt,
+                       lssm_dtype act);
+
 /* hidden[i, :] = table[ids[i], :]  (Mamba2Model::embed, mamba2_model.cpp:128-137). */
 int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out,
                uint32_t n, uint32_t d_model, uint32_t vocab, lssm_dtype act);

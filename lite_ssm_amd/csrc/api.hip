@@ -19,7 +19,7 @@ inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // 16-byte aligned weight rows, fp32 staging of <= 64 KiB per x row.
 bool gemv_ok(const void* w, uint32_t K, int wfmt, int act) {
     if (!al16(w)) return false;
-    if (K > 16384) return false;
+    if ((size_t)K * sizeof(float) > GEMV_LDS_BYTES) return false;
     switch (wfmt) {
         case LSSM_W_Q4_B32: return K % 32 == 0;
         case LSSM_W_Q4_G64: return K % 64 == 0;
@@ -231,11 +231,43 @@ int lssm_ssd_step(lssm_ctx* ctx, const void* x, const void* B, const void* C, co
     return finish(ctx, "ssd_step");
 }
 
+int lssm_inproj_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, const void* w,
+                       const void* w_scales, void* conv_state, const void* conv_w,
+                       const void* conv_b, void* z, void* xbc_act, void* dt, uint32_t batch,
+                       uint32_t d_model, uint32_t d_inner, uint32_t d_state, uint32_t n_groups,
+                       uint32_t n_heads, uint32_t d_conv, float eps, lssm_wfmt wfmt,
+                       lssm_dtype act) {
+    LSSM_CHECK_CTX(ctx);
+    LSSM_REQUIRE(valid_act(act), "inproj_decode: unknown dtype");
+    if (int rc = check_fmt_k(d_model, wfmt, w_scales)) return rc;
+    LSSM_REQUIRE(batch >= 1 && batch <= 4, "inproj_decode: batch must be in [1, 4]");
+    LSSM_REQUIRE(d_conv >= 1, "inproj_decode: d_conv must be >= 1");
+    LSSM_REQUIRE(gemv_ok(w, d_model, wfmt, act), "inproj_decode: unsupported d_model / weight alignment");
+    LSSM_REQUIRE((size_t)batch * d_model * 4 <= GEMV_LDS_BYTES, "inproj_decode: batch * d_model too large");
+    const uint32_t xbc = d_inner + 2u * n_groups * d_state;
+    InprojDecodeArgs a;
+    a.g = GemvArgs{hidden, d_model, w, w_scales, nullptr, 0, nullptr, norm_w, eps, batch,
+                   d_inner + xbc + n_heads, d_model, wfmt, act, LSSM_EPI_NONE};
+    a.d_inner = d_inner;
+    a.xbc = xbc;
+    a.H = n_heads;
+    a.dconv = d_conv;
+    a.conv_state = conv_state;
+    a.conv_w = conv_w;
+    a.conv_b = conv_b;
+    a.z = z;
+    a.xbc_act = xbc_act;
+    a.dt = dt;
+    hipError_t e = launch_inproj_decode(ctx->stream, a);
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "inproj_decode: %s", hipGetErrorString(e));
+    return finish(ctx, "inproj_decode");
+}
+
 int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out, uint32_t n,
                uint32_t d_model, uint32_t vocab, lssm_dtype act) {
     LSSM_CHECK_CTX(ctx);
     LSSM_REQUIRE(valid_act(act), "embed: unknown dtype");
-    LSSM_REQUIRE(n <= 65535, "embed: n must be <= 65535");
+    
     hipError_t e = launch_embed(ctx->stream, table, ids, out, n, d_model, vocab, act);
     if (e != hipSuccess) return set_error(LSSM_EDEVICE, "embed: %s", hipGetErrorString(e));
     return finish(ctx, "embed");

@@ -191,12 +191,15 @@ __global__ void conv1d_seed_kernel(const T* __restrict__ xBC, uint32_t xs, T* __
 // API rejects them before launch; this only guards the device read).
 template <typename T>
 __global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restrict__ ids,
-                             T* __restrict__ out, uint32_t d_model, uint32_t vocab) {
-    const uint32_t i = blockIdx.y;
-    const int32_t id = ids[i];
-    const bool ok = id >= 0 && (uint32_t)id < vocab;
-    for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < d_model; c += gridDim.x * blockDim.x)
-        out[(size_t)i * d_model + c] = ok ? table[(size_t)id * d_model + c] : from_f<T>(0.0f);
+                             T* __restrict__ out, uint32_t n, uint32_t d_model, uint32_t vocab) {
+    const size_t total = (size_t)n * d_model;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const size_t i = e / d_model, c = e % d_model;
+        const int32_t id = ids[i];
+        const bool ok = id >= 0 && (uint32_t)id < vocab;
+        out[e] = ok ? table[(size_t)id * d_model + c] : from_f<T>(0.0f);
+    }
 }
 
 // sampler.cpp:13-21: first index of the maximum.  (v, i) beats (v', i') iff
@@ -383,10 +386,11 @@ hipError_t launch_conv1d_keep_last(hipStream_t s, void* state, uint32_t n_window
 hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, void* out, uint32_t n,
                         uint32_t d_model, uint32_t vocab, int act) {
     if (n == 0) return hipSuccess;
-    dim3 grid(cdiv(d_model, NT), n);
+    const size_t total = (size_t)n * d_model;
+    const unsigned blocks = (unsigned)((total + NT - 1) / NT < 65536 ? (total + NT - 1) / NT : 65536);
     LSSM_DISPATCH_ACT(act, T,
-                      embed_kernel<T><<<grid, NT, 0, s>>>((const T*)table, ids, (T*)out, d_model,
-                                                          vocab));
+                      embed_kernel<T><<<blocks, NT, 0, s>>>((const T*)table, ids, (T*)out, n,
+                                                            d_model, vocab));
     return hipGetLastError();
 }
 

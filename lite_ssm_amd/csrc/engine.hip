@@ -102,7 +102,7 @@ struct lssm_engine {
     // Logits of `rows` hidden rows (row stride xs) -> logits, then argmax.
     hipError_t logits_argmax(const void* x, uint32_t xs, uint32_t rows, int32_t* next) const {
         hipError_t e;
-        if (rows <= 4 && (size_t)rows * d_model * 4 <= 64 * 1024) {
+        if (rows <= 4 && (size_t)rows * d_model * 4 <= GEMV_LDS_BYTES) {
             GemvArgs g{x, xs, lm_head, nullptr, logits, vocab, nullptr, norm_f, RMS_EPS, rows, vocab,
                        d_model, LSSM_W_DENSE, act, LSSM_EPI_NONE};
             e = launch_gemv(st(), g);
@@ -119,8 +119,8 @@ struct lssm_engine {
     // One decode step: ids -> next (all on device).  mamba2_block.cpp:317-327.
     hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
         hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act);
-        const bool fused_in = (size_t)B * d_model * 4 <= 64 * 1024 && B <= 4;
-        const bool fused_out = (size_t)B * d_inner * 4 <= 64 * 1024 && B <= 4;
+        const bool fused_in = (size_t)B * d_model * 4 <= GEMV_LDS_BYTES && B <= 4;
+        const bool fused_out = (size_t)B * d_inner * 4 <= GEMV_LDS_BYTES && B <= 4;
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
             char* cs = conv_layer(li);
@@ -298,6 +298,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
                  "engine_create: d_model and d_inner must be multiples of 64");
     LSSM_REQUIRE(cfg->d_model <= 16384 && d_inner <= 16384, "engine_create: d_model/d_inner > 16384");
     LSSM_REQUIRE(cfg->chunk_size >= 1, "engine_create: chunk_size must be >= 1");
+    LSSM_REQUIRE(max_seq <= 65535, "engine_create: max_seq must be <= 65535");
 
     auto* e = new lssm_engine();
     e->ctx = ctx;

@@ -24,7 +24,7 @@ constexpr int GV_NT = 256;
 constexpr int GV_LPR = 16;                       // lanes per weight row
 constexpr int GV_ROWS = GV_NT / GV_LPR;          // rows per block
 constexpr int GV_U = 4;                          // chunks in flight per lane
-constexpr size_t GV_LDS_MAX = 64 * 1024;
+constexpr size_t GV_LDS_MAX = GEMV_LDS_BYTES;
 
 struct GemvCore {
     const void* x;
@@ -215,11 +215,12 @@ template <int FMT, typename T, int MR, bool NORM, class Epi>
 hipError_t launch_one(hipStream_t s, const GemvCore& c, const Epi& e) {
     const size_t lds = (size_t)MR * c.K * sizeof(float);
     auto kern = gemv_kernel<FMT, T, MR, NORM, Epi>;
-    if (lds > 48 * 1024) {
-        hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (err != hipSuccess) return err;
-    }
+    // opt in to the full 64 KiB of dynamic LDS once per instantiation (a host
+    // attribute, done before any graph capture reaches this launch)
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)GV_LDS_MAX);
+    if (attr != hipSuccess) return attr;
     dim3 grid((c.N + GV_ROWS - 1) / GV_ROWS);
     kern<<<grid, GV_NT, lds, s>>>(c, e);
     return hipGetLastError();

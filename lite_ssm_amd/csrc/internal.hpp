@@ -32,6 +32,9 @@ void clear_error();
 // report asynchronous kernel failures.
 int finish(lssm_ctx* ctx, const char* what);
 
+// Dynamic LDS of the GEMV x staging (fp32 rows); static + dynamic stays <= 64 KiB.
+constexpr size_t GEMV_LDS_BYTES = 60 * 1024;
+
 inline size_t dtype_size(int act) { return act == LSSM_F32 ? 4 : 2; }
 inline bool valid_act(int act) { return act == LSSM_F16 || act == LSSM_BF16 || act == LSSM_F32; }
 inline bool valid_wfmt(int f) {

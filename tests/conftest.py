@@ -24,7 +24,11 @@ def torch_cuda():
 @pytest.fixture(scope="session")
 def ctx(torch_cuda):
     import lite_ssm_amd as L
-    c = L.Ctx(stream=torch_cuda.cuda.current_stream().cuda_stream)
+    # a dedicated (default-priority) stream shared by torch copies and the
+    # library, so ordering is implicit and HIP-graph capture is legal
+    s = torch_cuda.cuda.Stream()
+    torch_cuda.cuda.set_stream(s)
+    c = L.Ctx(stream=s.cuda_stream)
     yield c
     c.close()
 
@@ -32,3 +36,13 @@ def ctx(torch_cuda):
 @pytest.fixture
 def rng():
     return np.random.default_rng(1234)
+
+
+@pytest.fixture(autouse=True)
+def _keep_device_copies():
+    yield
+    try:
+        import gpu_util
+        gpu_util.KEEP.clear()
+    except ImportError:
+        pass

@@ -1,0 +1,195 @@
+"""Whole-model parity: the engine (fused decode kernels, MFMA prefill, HIP
+graph replay) against the oracle's restatement of Mamba2Model::run_block
+(mamba2_block.cpp:51-327) on the same random-init weights and token ids.
+
+Decode is teacher-forced: both sides are fed the oracle's greedy token, so a
+near-tie flip cannot make the sequences diverge; every step's logits are
+compared (max-rel 2e-2 for fp16 / bf16, 1e-3 for fp32), and the greedy ids
+must agree wherever the oracle's top-2 margin exceeds the comparison bound.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import MAXREL, max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(ctx, name, act, wfmt, seed=11, **over):
+    import lite_ssm_amd as L
+    from lite_ssm_amd.model import DeviceModel, shape
+    sh = shape(name, **over)
+    m = DeviceModel(sh, act=act, wfmt=wfmt, seed=seed)
+    om = O.Model(m.to_host(), vars(sh), act, wfmt)
+    return L, sh, m, om
+
+
+def _check_logits(gpu, ref_bits, act, what):
+    ref = O.from_act(ref_bits, act)
+    e = max_rel(gpu, ref)
+    assert np.all(np.isfinite(gpu)), what
+    assert e <= MAXREL[act], f"{what}: logits max-rel {e:.3e}"
+    # greedy ids agree wherever the top-2 margin is clear of the error bound
+    for r in range(ref.shape[0]):
+        top2 = np.sort(ref[r])[-2:]
+        if top2[1] - top2[0] > 4 * e * np.abs(ref).max():
+            assert int(np.argmax(gpu[r])) == int(np.argmax(ref[r])), f"{what}: greedy id row {r}"
+    return e
+
+
+CASES = [
+    ("f16-q8g32", O.F16, O.W_Q8_G32),     # config 3 formats
+    ("bf16-q4g64", O.BF16, O.W_Q4_G64),   # configs 4/5 formats
+    ("f16-q4b32", O.F16, O.W_Q4_B32),     # the reference's INT4_B32
+    ("f16-dense", O.F16, O.W_DENSE),      # the reference's fp16 checkpoints
+    ("f32-dense", O.F32, O.W_DENSE),
+]
+
+
+@pytest.mark.parametrize("tag,act,wfmt", CASES, ids=[c[0] for c in CASES])
+def test_engine_prefill_then_decode_vs_oracle(ctx, tag, act, wfmt):
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-130m", act, wfmt, n_layer=2, vocab_size=2048)
+    B, Lq = 2, 100
+    eng = Engine(ctx, m, max_batch=B, max_seq=Lq)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, sh.vocab_size, (B, Lq), generator=g, dtype=torch.int32)
+    nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+    eng.prefill(ids.cuda(), nxt)
+    conv, ssd = om.new_state(B)
+    ref = om.prefill(conv, ssd, ids.numpy())
+    _check_logits(eng.logits(B).float().cpu().numpy(), ref, act, f"{tag} prefill")
+    # the engine's greedy ids are the argmax of its own logits
+    assert list(nxt.cpu().numpy()) == list(np.argmax(eng.logits(B).float().cpu().numpy(), -1))
+    gconv, gssd = eng.state()
+    assert max_rel(gssd.cpu().numpy(), ssd) < MAXREL[act]
+    tok = O.argmax(ref, act)
+    for step in range(3):
+        eng.decode(torch.from_numpy(tok).cuda(), nxt)
+        ref = om.decode(conv, ssd, tok)
+        _check_logits(eng.logits(B).float().cpu().numpy(), ref, act, f"{tag} decode {step}")
+        tok = O.argmax(ref, act)
+    eng.close()
+
+
+def test_engine_graph_replay_matches_eager(ctx):
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-130m", O.BF16, O.W_Q4_G64, n_layer=3, vocab_size=1024)
+    eng = Engine(ctx, m, max_batch=1, max_seq=64)
+    ids = torch.randint(0, sh.vocab_size, (1, 64), dtype=torch.int32).cuda()
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    eng.prefill(ids, tok)
+    conv0, ssd0 = eng.state()
+    # eager: 5 steps feeding back the engine's own greedy ids
+    t_e = tok.clone()
+    eager = []
+    for _ in range(5):
+        eng.decode(t_e, t_e)
+        eager.append(int(t_e.item()))
+    conv_e, ssd_e = eng.state()
+    lg_e = eng.logits(1)
+    # graph: restore the post-prefill state, replay 5 steps
+    eng.reset()
+    eng.prefill(ids, tok)
+    t_g = tok.clone()
+    graph = []
+    for _ in range(5):
+        eng.decode_graph(t_g, t_g, 1)
+        graph.append(int(t_g.item()))
+    conv_g, ssd_g = eng.state()
+    assert graph == eager
+    assert torch.equal(ssd_g, ssd_e) and torch.equal(conv_g, conv_e)
+    assert torch.equal(eng.logits(1), lg_e)
+    eng.close()
+
+
+def test_engine_batch8_decode_uses_gemm_path(ctx):
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-130m", O.BF16, O.W_Q4_G64, n_layer=2, vocab_size=1024)
+    B = 8
+    eng = Engine(ctx, m, max_batch=B, max_seq=70)
+    ids = np.random.default_rng(2).integers(0, sh.vocab_size, (B, 70)).astype(np.int32)
+    nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+    eng.prefill(torch.from_numpy(ids).cuda(), nxt)
+    conv, ssd = om.new_state(B)
+    ref = om.prefill(conv, ssd, ids)
+    _check_logits(eng.logits(B).float().cpu().numpy(), ref, O.BF16, "b8 prefill")
+    tok = O.argmax(ref, O.BF16)
+    for step in range(2):
+        eng.decode(torch.from_numpy(tok).cuda(), nxt)
+        ref = om.decode(conv, ssd, tok)
+        _check_logits(eng.logits(B).float().cpu().numpy(), ref, O.BF16, f"b8 decode {step}")
+        tok = O.argmax(ref, O.BF16)
+    eng.close()
+
+
+def test_engine_one_token_prefill(ctx):
+    """L == 1 prefill takes the reference's GEMV / conv-update / SSD-step path
+    and seeds the conv state (mamba2_block.cpp:111-116, 155-162, 183-195, 285-289)."""
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-130m", O.F16, O.W_Q4_B32, n_layer=2, vocab_size=1024)
+    eng = Engine(ctx, m, max_batch=1, max_seq=8)
+    nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    eng.prefill(torch.tensor([[17]], dtype=torch.int32).cuda(), nxt)
+    conv, ssd = om.new_state(1)
+    ref = om.prefill(conv, ssd, np.array([[17]], np.int32))
+    _check_logits(eng.logits(1).float().cpu().numpy(), ref, O.F16, "L1 prefill")
+    gconv, _ = eng.state()
+    assert np.array_equal(gconv.cpu().view(torch.int16).numpy().view(np.uint16), conv)
+    eng.close()
+
+
+def test_engine_2p7b_layer_shapes(ctx):
+    """Full-width Mamba-2-2.7B layers (d_model 2560, 80 heads, int4 group-64,
+    bf16): 2 layers, reduced vocab, prefill 130 tokens at batch 2 + 2 decode steps."""
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-2.7b", O.BF16, O.W_Q4_G64, n_layer=2, vocab_size=512)
+    B, Lq = 2, 130
+    eng = Engine(ctx, m, max_batch=B, max_seq=Lq)
+    ids = np.random.default_rng(3).integers(0, sh.vocab_size, (B, Lq)).astype(np.int32)
+    nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+    eng.prefill(torch.from_numpy(ids).cuda(), nxt)
+    conv, ssd = om.new_state(B)
+    ref = om.prefill(conv, ssd, ids)
+    _check_logits(eng.logits(B).float().cpu().numpy(), ref, O.BF16, "2.7b prefill")
+    tok = O.argmax(ref, O.BF16)
+    for step in range(2):
+        eng.decode(torch.from_numpy(tok).cuda(), nxt)
+        ref = om.decode(conv, ssd, tok)
+        _check_logits(eng.logits(B).float().cpu().numpy(), ref, O.BF16, f"2.7b decode {step}")
+        tok = O.argmax(ref, O.BF16)
+    eng.close()
+
+
+def test_engine_8b_groups(ctx):
+    """Mamba-2-8B layer shapes (d_model 4096, 128 heads, 8 groups), 1 layer."""
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-8b", O.BF16, O.W_Q4_G64, n_layer=1, vocab_size=512)
+    B, Lq = 1, 80
+    eng = Engine(ctx, m, max_batch=B, max_seq=Lq)
+    ids = np.random.default_rng(4).integers(0, sh.vocab_size, (B, Lq)).astype(np.int32)
+    nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+    eng.prefill(torch.from_numpy(ids).cuda(), nxt)
+    conv, ssd = om.new_state(B)
+    ref = om.prefill(conv, ssd, ids)
+    _check_logits(eng.logits(B).float().cpu().numpy(), ref, O.BF16, "8b prefill")
+    tok = O.argmax(ref, O.BF16)
+    eng.decode(torch.from_numpy(tok).cuda(), nxt)
+    ref = om.decode(conv, ssd, tok)
+    _check_logits(eng.logits(B).float().cpu().numpy(), ref, O.BF16, "8b decode")
+    eng.close()
+
+
+def test_engine_argument_errors(ctx):
+    import lite_ssm_amd as L
+    from lite_ssm_amd.model import Engine
+    _, sh, m, _ = _setup(ctx, "mamba2-130m", O.F16, O.W_Q8_G32, n_layer=1, vocab_size=256)
+    eng = Engine(ctx, m, max_batch=1, max_seq=8)
+    nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    with pytest.raises(L.LssmError, match="exceeds workspace max_seq_len"):
+        eng.prefill(torch.zeros(1, 9, dtype=torch.int32, device="cuda"), nxt)
+    with pytest.raises(L.LssmError, match="batch out of range"):
+        eng.decode(torch.zeros(2, dtype=torch.int32, device="cuda"), nxt)
+    eng.close()

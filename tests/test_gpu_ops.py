@@ -1,0 +1,394 @@
+"""GPU parity of every op, through the C ABI, against the CPU oracle on the
+same seeded inputs (BASELINE configs 1 and 2 included at their full shapes)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import MAXREL, act_host, assert_close, dev, empty, host, max_rel, ulp_diff16
+
+pytestmark = pytest.mark.gpu
+
+ACTS = [O.F16, O.BF16, O.F32]
+QFMTS = [O.W_Q4_B32, O.W_Q4_G64, O.W_Q8_G32]
+ALL_FMTS = [O.W_DENSE] + QFMTS
+
+
+def _lib():
+    import lite_ssm_amd as L
+    return L
+
+
+def _weights(rng, N, K, wfmt, act, std=0.02):
+    wf = (rng.standard_normal((N, K)) * std).astype(np.float16).astype(np.float32)
+    if wfmt == O.W_DENSE:
+        return O.to_act(wf, act), None
+    return O.quantize(wf, wfmt)
+
+
+# --------------------------------------------------------------------------- dequant
+@pytest.mark.parametrize("wfmt", QFMTS)
+def test_dequant_bit_exact(ctx, rng, wfmt):
+    N, K = 96, 512
+    w, s = _weights(rng, N, K, wfmt, O.F16, std=1.0)
+    out = torch.empty(N, K, dtype=torch.float32, device="cuda")
+    ctx.dequant(dev(w), dev(s), out, N, K, wfmt)
+    ref = O.dequant(w, s, N, K, wfmt)
+    assert np.array_equal(host(out, np.float32).view(np.uint32), ref.view(np.uint32))
+
+
+# --------------------------------------------------------------------------- GEMV / GEMM
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("wfmt", ALL_FMTS)
+@pytest.mark.parametrize("M", [1, 3, 4])
+def test_gemv_vs_oracle(ctx, rng, act, wfmt, M):
+    L = _lib()
+    N, K = 200, 768
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    y = empty((M, N), act)
+    ctx.linear(dev(x), dev(w), None if s is None else dev(s), y, M, N, K, wfmt, act)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act)
+    got = act_host(y, act)
+    bound = {O.F16: 2e-3, O.BF16: 1.6e-2, O.F32: 1e-5}[act]
+    assert_close(got, ref, act, bound, "gemv")
+    if act == O.F16:
+        assert ulp_diff16(got, ref).max() <= 2
+
+
+@pytest.mark.parametrize("act", [O.F16, O.BF16])
+@pytest.mark.parametrize("wfmt", ALL_FMTS)
+@pytest.mark.parametrize("M", [5, 300])
+def test_gemm_vs_oracle(ctx, rng, act, wfmt, M):
+    N, K = 300, 1536
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    y = empty((M, N), act)
+    ctx.linear(dev(x), dev(w), None if s is None else dev(s), y, M, N, K, wfmt, act)
+    # GEMM semantics: dequantized weight rounded to the activation dtype (linear.metal:538)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, round_dequant=1)
+    bound = {O.F16: 2e-3, O.BF16: 1.6e-2}[act]
+    assert_close(act_host(y, act), ref, act, bound, "gemm")
+
+
+@pytest.mark.parametrize("act", [O.F16, O.BF16, O.F32])
+@pytest.mark.parametrize("M", [2, 130])
+def test_linear_epilogues(ctx, rng, act, M):
+    L = _lib()
+    N, K, wfmt = 256, 512, O.W_Q4_G64
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    res = O.to_act(rng.standard_normal((M, N)), act)
+    yd = dev(res)                                   # in-place residual: y == residual
+    ctx.linear(dev(x), dev(w), dev(s), yd, M, N, K, wfmt, act, epi=L.EPI_ADD, residual=yd)
+    rd = 1 if M > 4 else 0
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, epi=O.EPI_ADD, residual=res, round_dequant=rd)
+    assert_close(act_host(yd, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2, O.F32: 1e-5}[act], "add")
+    ys = empty((M, N), act)
+    ctx.linear(dev(x), dev(w), dev(s), ys, M, N, K, wfmt, act, epi=L.EPI_SILU)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, epi=O.EPI_SILU, round_dequant=rd)
+    assert_close(act_host(ys, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2, O.F32: 1e-5}[act], "silu")
+
+
+@pytest.mark.parametrize("which", ["in_proj", "out_proj"])
+def test_config2_q8g32_130m_shapes_gemv_and_gemm(ctx, rng, which):
+    """130M in_proj [3352 x 768] / out_proj [768 x 1536],
+    int8 group-32 fp16 scales, N(0, 0.02) weights, fp16 activations; M = 1 and 2048."""
+    N, K = (3352, 768) if which == "in_proj" else (768, 1536)
+    w, s = _weights(rng, N, K, O.W_Q8_G32, O.F16)
+    wd, sd = dev(w), dev(s)
+    for M in (1, 2048):
+        x = O.to_act(rng.standard_normal((M, K)), O.F16)
+        y = empty((M, N), O.F16)
+        ctx.linear(dev(x), wd, sd, y, M, N, K, O.W_Q8_G32, O.F16)
+        ref = O.linear(x, w, s, M, N, K, O.W_Q8_G32, O.F16, round_dequant=int(M > 4))
+        assert_close(act_host(y, O.F16), ref, O.F16, 2e-3, f"config2 {which} M={M}")
+
+
+def test_reference_named_linear_entries(ctx, rng):
+    L = _lib()
+    lib = L.lib
+    N, K = 100, 256
+    x1 = O.to_act(rng.standard_normal((1, K)), O.F16)
+    x8 = O.to_act(rng.standard_normal((8, K)), O.F16)
+    w4, s4 = _weights(rng, N, K, O.W_Q4_B32, O.F16)
+    wh, _ = _weights(rng, N, K, O.W_DENSE, O.F16)
+    y1, y8 = empty((1, N), O.F16), empty((8, N), O.F16)
+    L.check(lib.lssm_linear_int4_gemv(ctx.h, dev(x1).data_ptr(), dev(w4).data_ptr(), dev(s4).data_ptr(),
+                                      y1.data_ptr(), L.LinearDims(1, N, K)))
+    assert_close(act_host(y1, O.F16), O.linear(x1, w4, s4, 1, N, K, O.W_Q4_B32, O.F16), O.F16, 2e-3)
+    L.check(lib.lssm_linear_int4_gemm(ctx.h, dev(x8).data_ptr(), dev(w4).data_ptr(), dev(s4).data_ptr(),
+                                      y8.data_ptr(), L.LinearDims(8, N, K)))
+    assert_close(act_host(y8, O.F16), O.linear(x8, w4, s4, 8, N, K, O.W_Q4_B32, O.F16, round_dequant=1),
+                 O.F16, 2e-3)
+    for fn, epi in ((lib.lssm_linear_f16_gemv, O.EPI_NONE), (lib.lssm_linear_silu_f16_gemv, O.EPI_SILU)):
+        L.check(fn(ctx.h, dev(x1).data_ptr(), dev(wh).data_ptr(), y1.data_ptr(), L.LinearDims(1, N, K)))
+        assert_close(act_host(y1, O.F16), O.linear(x1, wh, None, 1, N, K, O.W_DENSE, O.F16, epi=epi), O.F16, 2e-3)
+    for fn, epi in ((lib.lssm_linear_f16_gemm, O.EPI_NONE), (lib.lssm_linear_silu_f16_gemm, O.EPI_SILU)):
+        L.check(fn(ctx.h, dev(x8).data_ptr(), dev(wh).data_ptr(), y8.data_ptr(), L.LinearDims(8, N, K)))
+        assert_close(act_host(y8, O.F16), O.linear(x8, wh, None, 8, N, K, O.W_DENSE, O.F16, epi=epi), O.F16, 2e-3)
+    # rmsnorm_linear_f16_gemv (linear.metal:148-204): normed rounded to half, then GEMV
+    wn = O.to_act(1 + 0.1 * rng.standard_normal(K), O.F16)
+    L.check(lib.lssm_rmsnorm_linear_f16_gemv(ctx.h, dev(x1).data_ptr(), dev(wn).data_ptr(),
+                                             dev(wh).data_ptr(), y1.data_ptr(), L.RMSLinearDims(N, K, 1e-5)))
+    ref = O.linear(O.rmsnorm(x1, wn, 1e-5, O.F16), wh, None, 1, N, K, O.W_DENSE, O.F16)
+    assert_close(act_host(y1, O.F16), ref, O.F16, 2e-3)
+    # preconditions keep the reference's messages (ops.mm:207-212, 323-324)
+    rc = lib.lssm_linear_int4_gemv(ctx.h, dev(x8).data_ptr(), dev(w4).data_ptr(), dev(s4).data_ptr(),
+                                   y8.data_ptr(), L.LinearDims(8, N, K))
+    assert rc == 1 and b"M must be 1" in lib.lssm_last_error()
+    rc = lib.lssm_linear_int4_gemv(ctx.h, dev(x1).data_ptr(), dev(w4).data_ptr(), dev(s4).data_ptr(),
+                                   y1.data_ptr(), L.LinearDims(1, N, 250))
+    assert rc == 1 and b"multiple of 32" in lib.lssm_last_error()
+    rc = lib.lssm_rmsnorm_f16(ctx.h, None, None, None, L.RMSNormDims(1, 6, 1e-5))
+    assert rc == 1 and b"multiple of 4" in lib.lssm_last_error()
+
+
+# --------------------------------------------------------------------------- norms / activations
+@pytest.mark.parametrize("act", ACTS)
+def test_rmsnorm_and_gated(ctx, rng, act):
+    L = _lib()
+    rows, dim = 7, 1536
+    x = O.to_act(rng.standard_normal((rows, dim)) * 2, act)
+    z = O.to_act(rng.standard_normal((rows, dim)), act)
+    w = O.to_act(1 + 0.1 * rng.standard_normal(dim), act)
+    y = empty((rows, dim), act)
+    ctx.rmsnorm(dev(x), dev(w), y, rows, dim, 1e-5, act)
+    ref = O.rmsnorm(x, w, 1e-5, act)
+    assert_close(act_host(y, act), ref, act, {O.F16: 1e-3, O.BF16: 8e-3, O.F32: 1e-6}[act], "rmsnorm")
+    L.check(L.lib.lssm_gated_rmsnorm(ctx.h, dev(z).data_ptr(), dev(x).data_ptr(), dev(w).data_ptr(),
+                                     y.data_ptr(), rows, dim, 1e-5, act))
+    ref = O.gated_rmsnorm(z, x, w, 1e-5, act)
+    assert_close(act_host(y, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2, O.F32: 1e-6}[act], "gated")
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_elementwise(ctx, rng, act):
+    L = _lib()
+    lib = L.lib
+    n = 5000
+    a = O.to_act(rng.standard_normal(n) * 3, act)
+    b = O.to_act(rng.standard_normal(n), act)
+    y = empty((n,), act)
+    L.check(lib.lssm_silu(ctx.h, dev(a).data_ptr(), y.data_ptr(), n, act))
+    assert_close(act_host(y, act), O.silu(a, act), act, {O.F16: 1e-3, O.BF16: 8e-3, O.F32: 1e-6}[act])
+    L.check(lib.lssm_silu_gated(ctx.h, dev(a).data_ptr(), dev(b).data_ptr(), y.data_ptr(), n, act))
+    assert_close(act_host(y, act), O.silu_gated(a, b, act), act, {O.F16: 1e-3, O.BF16: 8e-3, O.F32: 1e-6}[act])
+    yd = dev(a)
+    L.check(lib.lssm_add_inplace(ctx.h, yd.data_ptr(), dev(b).data_ptr(), n, act))
+    assert np.array_equal(act_host(yd, act), O.add_inplace(a.copy(), b, act))
+    rows, d_inner, N, G = 9, 256, 64, 2
+    xbc = O.to_act(rng.standard_normal((rows, d_inner + 2 * G * N)) * 3, act)
+    xo, Bo, Co = empty((rows, d_inner), act), empty((rows, G * N), act), empty((rows, G * N), act)
+    L.check(lib.lssm_split_silu_xbc(ctx.h, dev(xbc).data_ptr(), xo.data_ptr(), Bo.data_ptr(),
+                                    Co.data_ptr(), rows, d_inner, N, G, act))
+    for g_, r_ in zip((xo, Bo, Co), O.split_silu_xbc(xbc, rows, d_inner, N, G, act)):
+        assert_close(act_host(g_, act), r_, act, {O.F16: 1e-3, O.BF16: 8e-3, O.F32: 1e-6}[act], "split")
+
+
+# --------------------------------------------------------------------------- conv
+@pytest.mark.parametrize("act", ACTS)
+def test_conv1d_family(ctx, rng, act):
+    L = _lib()
+    lib = L.lib
+    B, Lq, D, K = 2, 37, 1792, 4
+    x = O.to_act(rng.standard_normal((B, Lq, D)), act)
+    w = O.to_act(rng.standard_normal((D, K)) * 0.5, act)
+    bb = O.to_act(rng.standard_normal(D) * 0.1, act)
+    y = empty((B, Lq, D), act)
+    L.check(lib.lssm_conv1d(ctx.h, dev(x).data_ptr(), dev(w).data_ptr(), dev(bb).data_ptr(), y.data_ptr(),
+                            B, Lq, D, K, act))
+    ref = O.conv1d(x, w, bb, B, Lq, D, K, act)
+    assert_close(act_host(y, act), ref, act, {O.F16: 1e-3, O.BF16: 8e-3, O.F32: 1e-6}[act], "conv1d")
+    st = empty((B, D, K), act)
+    L.check(lib.lssm_conv1d_seed(ctx.h, dev(x).data_ptr(), st.data_ptr(), B, Lq, D, K, act))
+    seed = O.conv1d_seed(x, B, Lq, D, K, act)
+    assert np.array_equal(act_host(st, act), seed)
+    xn = O.to_act(rng.standard_normal((B, D)), act)
+    yo = empty((B, D), act)
+    L.check(lib.lssm_conv1d_update(ctx.h, dev(xn).data_ptr(), st.data_ptr(), dev(w).data_ptr(),
+                                   dev(bb).data_ptr(), yo.data_ptr(), B, D, K, act))
+    seed2 = seed.copy()
+    yref = O.conv1d_update(xn, seed2, w, bb, B, D, K, act)
+    assert np.array_equal(act_host(st, act), seed2)
+    assert_close(act_host(yo, act), yref, act, {O.F16: 1e-3, O.BF16: 8e-3, O.F32: 1e-6}[act], "update")
+
+
+def test_reference_conv_entries_f16(ctx, rng):
+    L = _lib()
+    lib = L.lib
+    Lq, D, K = 12, 64, 4
+    x = O.to_act(rng.standard_normal((1, Lq, D)), O.F16)
+    w = O.to_act(rng.standard_normal((D, K)) * 0.5, O.F16)
+    bb = O.to_act(rng.standard_normal(D) * 0.1, O.F16)
+    y = empty((1, Lq, D), O.F16)
+    L.check(lib.lssm_causal_conv1d_f16(ctx.h, dev(x).data_ptr(), dev(w).data_ptr(), dev(bb).data_ptr(),
+                                       y.data_ptr(), L.Conv1dDims(1, Lq, D, K)))
+    assert_close(act_host(y, O.F16), O.conv1d(x, w, bb, 1, Lq, D, K, O.F16), O.F16, 1e-3)
+    st = empty((1, D, K), O.F16)
+    L.check(lib.lssm_seed_conv_state_f16(ctx.h, dev(x).data_ptr(), st.data_ptr(), Lq, D, K))
+    assert np.array_equal(act_host(st, O.F16), O.conv1d_seed(x, 1, Lq, D, K, O.F16))
+
+
+# --------------------------------------------------------------------------- SSD
+def _ssd_inputs(rng, batch, L, H, P, N, G, act):
+    X = O.to_act(rng.standard_normal((batch, L, H, P)), act)
+    B = O.to_act(rng.standard_normal((batch, L, G, N)) / np.sqrt(N), act)
+    Cc = O.to_act(rng.standard_normal((batch, L, G, N)) / np.sqrt(N), act)
+    dt = O.to_act(rng.normal(-2.0, 0.5, (batch, L, H)), act)        # softplus(N(-2, .5))
+    dtb = O.to_act(np.zeros(H), act)
+    A_log = O.to_act(rng.uniform(0, np.log(16), H), act)            # A = -exp(U(log 1, log 16))
+    D = O.to_act(rng.standard_normal(H), act)
+    return X, B, Cc, dt, dtb, A_log, D
+
+
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("G,H,batch", [(1, 24, 1), (8, 32, 3)])
+def test_ssd_step_vs_oracle(ctx, rng, act, G, H, batch):
+    L = _lib()
+    P, N = 64, 128
+    X, B, Cc, dt, dtb, A_log, D = _ssd_inputs(rng, batch, 1, H, P, N, G, act)
+    st = (rng.standard_normal((batch, H, P, N)) * 0.5).astype(np.float32)
+    xs, Bs, Cs, dts = (np.ascontiguousarray(a[:, 0]) for a in (X, B, Cc, dt))
+    sd = dev(st)
+    y = empty((batch, H, P), act)
+    ctx.ssd_step(dev(xs), dev(Bs), dev(Cs), dev(dts), dev(dtb), dev(A_log), dev(D), sd, y, batch,
+                 L.SSDStepDims(H, P, N, G, 1e-6, 1e6, 1), act)
+    s2 = st.copy()
+    yr = O.ssd_step(xs, Bs, Cs, dts, dtb, A_log, D, s2, batch, H, P, N, G, act)
+    assert max_rel(host(sd, np.float32), s2) < 1e-5
+    assert_close(act_host(y, act), yr, act, {O.F16: 2e-3, O.BF16: 1.6e-2, O.F32: 1e-5}[act], "ssd_step")
+
+
+def test_ssd_chunked_config1_fp32(ctx, rng):
+    """fp32 SSD, 130M layer shape: batch 1, L 512, 24 heads x 64,
+    d_state 128, 1 group, chunk 64.  max-rel 1e-3 on y and the final state."""
+    L = _lib()
+    act, batch, Lq, H, P, N, G = O.F32, 1, 512, 24, 64, 128, 1
+    X, B, Cc, dt, dtb, A_log, D = _ssd_inputs(rng, batch, Lq, H, P, N, G, act)
+    sd = torch.zeros(batch, H, P, N, dtype=torch.float32, device="cuda")
+    Y = empty((batch, Lq, H, P), act)
+    ctx.ssd_chunked(dev(X), dev(B), dev(Cc), dev(dt), dev(dtb), dev(A_log), dev(D), Y, sd, batch,
+                    L.SSDDims(Lq, H, P, N, G, 64, 1e-6, 1e6, 1), act)
+    s2 = np.zeros((batch, H, P, N), np.float32)
+    Yr = O.ssd_chunked(X, B, Cc, dt, dtb, A_log, D, s2, batch, Lq, H, P, N, G, 64, act)
+    assert max_rel(host(Y, np.float32), Yr) < 1e-3
+    assert max_rel(host(sd, np.float32), s2) < 1e-3
+
+
+@pytest.mark.parametrize("act", [O.F16, O.BF16])
+@pytest.mark.parametrize("batch,Lq,H,G", [(1, 512, 24, 1), (2, 200, 8, 2), (1, 40, 4, 1), (3, 64, 16, 8)])
+def test_ssd_chunked_mfma_vs_oracle(ctx, rng, act, batch, Lq, H, G):
+    L = _lib()
+    P, N = 64, 128
+    X, B, Cc, dt, dtb, A_log, D = _ssd_inputs(rng, batch, Lq, H, P, N, G, act)
+    st = (rng.standard_normal((batch, H, P, N)) * 0.2).astype(np.float32)
+    ck = min(64, Lq)
+    sd = dev(st)
+    Y = empty((batch, Lq, H, P), act)
+    ctx.ssd_chunked(dev(X), dev(B), dev(Cc), dev(dt), dev(dtb), dev(A_log), dev(D), Y, sd, batch,
+                    L.SSDDims(Lq, H, P, N, G, ck, 1e-6, 1e6, 1), act)
+    s2 = st.copy()
+    Yr = O.ssd_chunked(X, B, Cc, dt, dtb, A_log, D, s2, batch, Lq, H, P, N, G, ck, act)
+    assert_close(act_host(Y, act), Yr, act, 2e-2, "ssd_chunked y")
+    assert max_rel(host(sd, np.float32), s2) < 2e-2
+
+
+def test_ssd_chunked_reference_entry_and_checks(ctx, rng):
+    L = _lib()
+    lib = L.lib
+    Lq, H, P, N = 100, 4, 64, 128
+    X, B, Cc, dt, dtb, A_log, D = _ssd_inputs(rng, 1, Lq, H, P, N, 1, O.F16)
+    sd = torch.zeros(1, H, P, N, dtype=torch.float32, device="cuda")
+    Y = empty((1, Lq, H, P), O.F16)
+    args = [dev(a).data_ptr() for a in (X, B, Cc, dt, dtb, A_log, D)]
+    L.check(lib.lssm_ssd_chunked_f16(ctx.h, *args, Y.data_ptr(), sd.data_ptr(),
+                                     L.SSDDims(Lq, H, P, N, 1, 64, 1e-6, 1e6, 1)))
+    s2 = np.zeros((1, H, P, N), np.float32)
+    Yr = O.ssd_chunked(X, B, Cc, dt, dtb, A_log, D, s2, 1, Lq, H, P, N, 1, 64, O.F16)
+    assert_close(act_host(Y, O.F16), Yr, O.F16, 2e-2)
+    rc = lib.lssm_ssd_chunked_f16(ctx.h, *args, Y.data_ptr(), sd.data_ptr(),
+                                  L.SSDDims(Lq, H, P, N, 1, 128, 1e-6, 1e6, 1))
+    assert rc == 1 and b"chunk_size" in lib.lssm_last_error()
+
+
+# --------------------------------------------------------------------------- fused in_proj, embed, argmax
+def test_inproj_fused_vs_oracle(ctx, rng):
+    L = _lib()
+    Lq, d_model, d_inner, N, G, H, K = 12, 768, 1536, 128, 1, 24, 4
+    xbc = d_inner + 2 * G * N
+    proj = d_inner + xbc + H
+    normed = O.to_act(rng.standard_normal((Lq, d_model)), O.F16)
+    W = O.to_act(rng.standard_normal((proj, d_model)) * 0.02, O.F16)
+    Wc = O.to_act(rng.standard_normal((xbc, K)) * 0.5, O.F16)
+    cb = O.to_act(rng.standard_normal(xbc) * 0.1, O.F16)
+    outs = [empty(s, O.F16) for s in ((Lq, d_inner), (Lq, d_inner), (Lq, G * N), (Lq, G * N), (Lq, H), (Lq, xbc))]
+    L.check(L.lib.lssm_inproj_fused_f16(ctx.h, dev(normed).data_ptr(), dev(W).data_ptr(),
+                                        dev(Wc).data_ptr(), dev(cb).data_ptr(),
+                                        *[o.data_ptr() for o in outs],
+                                        L.FusedInProjDims(Lq, d_model, d_inner, N, G, H, K, proj)))
+    refs = O.inproj_fused(normed, W, Wc, cb, Lq, d_model, d_inner, N, G, H, K)
+    for o, r in zip(outs, refs):
+        assert_close(act_host(o, O.F16), r, O.F16, 2e-3, "inproj_fused")
+
+
+@pytest.mark.parametrize("act,wfmt,batch", [(O.BF16, O.W_Q4_G64, 1), (O.F16, O.W_Q8_G32, 3),
+                                            (O.F16, O.W_Q4_B32, 4), (O.F32, O.W_DENSE, 2)])
+def test_inproj_decode_vs_unfused_chain(ctx, rng, act, wfmt, batch):
+    """The engine's fused decode in_proj == rmsnorm -> gemv -> conv update -> split SiLU."""
+    L = _lib()
+    d_model, d_inner, N, G, H, K = 2560, 5120, 128, 1, 80, 4
+    xbc = d_inner + 2 * G * N
+    proj = d_inner + xbc + H
+    hid = O.to_act(rng.standard_normal((batch, d_model)) * 0.5, act)
+    nw = O.to_act(1 + 0.1 * rng.standard_normal(d_model), act)
+    w, s = _weights(rng, proj, d_model, wfmt, act)
+    cw = O.to_act(rng.standard_normal((xbc, K)) * 0.3, act)
+    cb = O.to_act(rng.standard_normal(xbc) * 0.1, act)
+    cs = O.to_act(rng.standard_normal((batch, xbc, K)), act)
+    csd = dev(cs)
+    z, xa, dt = empty((batch, d_inner), act), empty((batch, xbc), act), empty((batch, H), act)
+    L.check(L.lib.lssm_inproj_decode(ctx.h, dev(hid).data_ptr(), dev(nw).data_ptr(), dev(w).data_ptr(),
+                                     None if s is None else dev(s).data_ptr(), csd.data_ptr(),
+                                     dev(cw).data_ptr(), dev(cb).data_ptr(), z.data_ptr(), xa.data_ptr(),
+                                     dt.data_ptr(), batch, d_model, d_inner, N, G, H, K, 1e-5, wfmt, act))
+    normed = O.rmsnorm(hid, nw, 1e-5, act)
+    pr = O.linear(normed, w, s, batch, proj, d_model, wfmt, act)
+    bound = {O.F16: 2e-3, O.BF16: 1.6e-2, O.F32: 1e-5}[act]
+    assert_close(act_host(z, act), np.ascontiguousarray(pr[:, :d_inner]), act, bound, "z")
+    assert_close(act_host(dt, act), np.ascontiguousarray(pr[:, d_inner + xbc:]), act, bound, "dt")
+    cs2 = cs.copy()
+    conv = O.conv1d_update(np.ascontiguousarray(pr[:, d_inner:d_inner + xbc]), cs2, cw, cb, batch, xbc, K, act)
+    ref = O.silu(conv, act)
+    assert_close(act_host(xa, act), ref, act, bound * 4, "xbc_act")
+    assert_close(act_host(csd, act), cs2, act, bound, "conv_state")
+
+
+@pytest.mark.parametrize("act", [O.F16, O.BF16])
+def test_embed_and_argmax(ctx, rng, act):
+    L = _lib()
+    vocab, d = 50280, 256
+    table = O.to_act(rng.standard_normal((vocab, d)), act)
+    ids = np.array([0, 5, 50279, 1234], np.int32)
+    out = empty((4, d), act)
+    L.check(L.lib.lssm_embed(ctx.h, dev(table).data_ptr(), dev(ids).data_ptr(), out.data_ptr(), 4, d,
+                             vocab, act))
+    assert np.array_equal(act_host(out, act), table[ids])
+    lg = O.to_act(rng.standard_normal((3, vocab)), act)
+    lg[1, 777] = lg[1, 40000] = O.to_act(np.array([99.0]), act)[0]      # tie -> first index
+    got = torch.zeros(3, dtype=torch.int32, device="cuda")
+    L.check(L.lib.lssm_argmax(ctx.h, dev(lg).data_ptr(), got.data_ptr(), 3, vocab, act))
+    assert list(host(got, np.int32)) == list(O.argmax(lg, act))
+    assert host(got, np.int32)[1] == 777
+
+
+def test_batch_lifecycle_errors(ctx):
+    L = _lib()
+    ctx.begin_batch()
+    assert ctx.batch_active()
+    with pytest.raises(L.LssmError, match="already active"):
+        ctx.begin_batch()
+    ctx.commit_and_wait()
+    with pytest.raises(L.LssmError, match="without an active batch"):
+        ctx.commit_and_wait()
+    assert L.lib.lssm_library_loaded() == 1
