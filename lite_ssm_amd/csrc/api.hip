@@ -242,8 +242,10 @@ int lssm_inproj_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, co
     if (int rc = check_fmt_k(d_model, wfmt, w_scales)) return rc;
     LSSM_REQUIRE(batch >= 1 && batch <= 4, "inproj_decode: batch must be in [1, 4]");
     LSSM_REQUIRE(d_conv >= 1, "inproj_decode: d_conv must be >= 1");
+    LSSM_REQUIRE((uintptr_t)conv_state % 8 == 0 && (uintptr_t)conv_w % 8 == 0,
+                 "inproj_decode: conv_state and conv_w must be 8-byte aligned");
     LSSM_REQUIRE(gemv_ok(w, d_model, wfmt, act), "inproj_decode: unsupported d_model / weight alignment");
-    LSSM_REQUIRE((size_t)batch * d_model * 4 <= GEMV_LDS_BYTES, "inproj_decode: batch * d_model too large");
+    LSSM_REQUIRE((int)batch <= gemv_max_rows(d_model, wfmt, act), "inproj_decode: batch * d_model too large");
     const uint32_t xbc = d_inner + 2u * n_groups * d_state;
     InprojDecodeArgs a;
     a.g = GemvArgs{hidden, d_model, w, w_scales, nullptr, 0, nullptr, norm_w, eps, batch,

@@ -102,7 +102,7 @@ struct lssm_engine {
     // Logits of `rows` hidden rows (row stride xs) -> logits, then argmax.
     hipError_t logits_argmax(const void* x, uint32_t xs, uint32_t rows, int32_t* next) const {
         hipError_t e;
-        if (rows <= 4 && (size_t)rows * d_model * 4 <= GEMV_LDS_BYTES) {
+        if (rows <= 4 && gemv_max_rows(d_model, LSSM_W_DENSE, act) >= 1) {
             GemvArgs g{x, xs, lm_head, nullptr, logits, vocab, nullptr, norm_f, RMS_EPS, rows, vocab,
                        d_model, LSSM_W_DENSE, act, LSSM_EPI_NONE};
             e = launch_gemv(st(), g);
@@ -119,8 +119,8 @@ struct lssm_engine {
     // One decode step: ids -> next (all on device).  mamba2_block.cpp:317-327.
     hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
         hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act);
-        const bool fused_in = (size_t)B * d_model * 4 <= GEMV_LDS_BYTES && B <= 4;
-        const bool fused_out = (size_t)B * d_inner * 4 <= GEMV_LDS_BYTES && B <= 4;
+        const bool fused_in = B <= 4 && (int)B <= gemv_max_rows(d_model, wfmt, act);
+        const bool fused_out = B <= 4 && gemv_max_rows(d_inner, wfmt, act) >= 1;
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
             char* cs = conv_layer(li);

@@ -19,53 +19,50 @@ namespace lssm {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Decode step.  Block (h, b), 256 threads.  The (P, N) fp32 state row block is
-// streamed once with 16-byte loads/stores: thread t owns float4 index
-// t + 256 i, i.e. row p = (t + 256 i) / (N/4) and 4 consecutive n.  The N/4
-// lanes sharing a row reduce C.s with shuffles.
+// Decode step.  Block (h * PS + ps, b), 256 threads, owns RB = 256 / (N/4)
+// rows p of one head's (P, N) fp32 state; each thread streams exactly one
+// float4 of state (one 16-byte load and store), so all of a block's loads are
+// independent and in flight together.  The N/4 lanes of a row reduce C.s with
+// shuffles.  P is spread over PS blocks to put H * PS * batch blocks on the
+// 256 CUs (bs=1, 2.7B: 640 blocks).
 // ---------------------------------------------------------------------------
 template <typename T, int NV, bool GATE>
 __global__ __launch_bounds__(256) void ssd_step_kernel(SsdArgs a) {
-    const uint32_t h = blockIdx.x, b = blockIdx.y;
+    constexpr uint32_t RB = 256 / NV;
     const uint32_t P = a.P, N = a.N;
+    const uint32_t PS = (P + RB - 1) / RB;
+    const uint32_t h = blockIdx.x / PS, ps = blockIdx.x % PS, b = blockIdx.y;
+    const uint32_t p = ps * RB + threadIdx.x / NV;
+    if (p >= P) return;                               // whole NV-lane row groups exit together
     const uint32_t hpg = (a.H / a.G) > 0 ? a.H / a.G : 1;
     const uint32_t g = h / hpg;
-    const T* X = (const T*)a.X + (size_t)b * a.x_stride + (size_t)h * P;
-    const T* Bv = (const T*)a.B + (size_t)b * a.b_stride + (size_t)g * N;
-    const T* Cv = (const T*)a.C + (size_t)b * a.c_stride + (size_t)g * N;
+    const uint32_t lr = threadIdx.x % NV;             // float4 column within the row
+    const uint32_t n = lr * 4;
+    float4* S = reinterpret_cast<float4*>(a.state + (((size_t)b * a.H + h) * P + p) * N) + lr;
+    float4 s = *S;
+    const T* Bv = (const T*)a.B + (size_t)b * a.b_stride + (size_t)g * N + n;
+    const T* Cv = (const T*)a.C + (size_t)b * a.c_stride + (size_t)g * N + n;
+    const float xv = to_f(((const T*)a.X)[(size_t)b * a.x_stride + (size_t)h * P + p]);
     const float A_h = -expf(to_f(((const T*)a.A_log)[h]));
     float dt = softplus_f(to_f(((const T*)a.dt)[(size_t)b * a.dt_stride + h]) + to_f(((const T*)a.dt_bias)[h]));
     dt = fminf(fmaxf(dt, a.dt_min), a.dt_max);
     const float decay = expf(A_h * dt);
     const float D_h = a.has_D ? to_f(((const T*)a.D)[h]) : 0.0f;
-    float4* S = reinterpret_cast<float4*>(a.state + (((size_t)b * a.H + h) * P) * N);
-
-    const uint32_t nv = P * N / 4;
-    const uint32_t lr = threadIdx.x % NV;           // float4 column within the row
-    const uint32_t n = lr * 4;
-    const float b0 = dt * to_f(Bv[n]), b1 = dt * to_f(Bv[n + 1]), b2 = dt * to_f(Bv[n + 2]),
-                b3 = dt * to_f(Bv[n + 3]);
-    const float c0 = to_f(Cv[n]), c1 = to_f(Cv[n + 1]), c2 = to_f(Cv[n + 2]), c3 = to_f(Cv[n + 3]);
-    for (uint32_t i = threadIdx.x; i < nv; i += 256) {
-        const uint32_t p = i / NV;
-        const float xv = to_f(X[p]);
-        float4 s = S[i];
-        // s = decay*s + (dt*B)*x  (ssd_step.metal:68-69)
-        s.x = decay * s.x + b0 * xv;
-        s.y = decay * s.y + b1 * xv;
-        s.z = decay * s.z + b2 * xv;
-        s.w = decay * s.w + b3 * xv;
-        S[i] = s;
-        float ys = c0 * s.x + c1 * s.y + c2 * s.z + c3 * s.w;
-        ys = group_sum<NV>(ys);
-        if (lr == 0) {
-            float y = rnd<T>(ys + D_h * xv);
-            if constexpr (GATE) {
-                const T* Z = (const T*)a.z + (size_t)b * a.z_stride + (size_t)h * P;
-                y = silu_f(to_f(Z[p])) * y;
-            }
-            ((T*)a.Y)[(size_t)b * a.y_stride + (size_t)h * P + p] = from_f<T>(y);
+    // s = decay*s + (dt*B)*x  (ssd_step.metal:68-69)
+    s.x = decay * s.x + dt * to_f(Bv[0]) * xv;
+    s.y = decay * s.y + dt * to_f(Bv[1]) * xv;
+    s.z = decay * s.z + dt * to_f(Bv[2]) * xv;
+    s.w = decay * s.w + dt * to_f(Bv[3]) * xv;
+    *S = s;
+    float ys = to_f(Cv[0]) * s.x + to_f(Cv[1]) * s.y + to_f(Cv[2]) * s.z + to_f(Cv[3]) * s.w;
+    ys = group_sum<NV>(ys);
+    if (lr == 0) {
+        float y = rnd<T>(ys + D_h * xv);
+        if constexpr (GATE) {
+            const T* Z = (const T*)a.z + (size_t)b * a.z_stride + (size_t)h * P;
+            y = silu_f(to_f(Z[p])) * y;
         }
+        ((T*)a.Y)[(size_t)b * a.y_stride + (size_t)h * P + p] = from_f<T>(y);
     }
 }
 
@@ -421,13 +418,13 @@ __global__ __launch_bounds__(MF_NT) void ssd_chunk_mfma_kernel(SsdArgs a) {
 
 template <typename T, bool GATE>
 hipError_t step_go(hipStream_t s, const SsdArgs& a) {
-    dim3 grid(a.H, a.batch);
     const uint32_t nv = a.N / 4;
-    const bool vec = (a.N % 4 == 0);
-    if (vec && nv == 32) ssd_step_kernel<T, 32, GATE><<<grid, 256, 0, s>>>(a);
-    else if (vec && nv == 16) ssd_step_kernel<T, 16, GATE><<<grid, 256, 0, s>>>(a);
-    else if (vec && nv == 64) ssd_step_kernel<T, 64, GATE><<<grid, 256, 0, s>>>(a);
-    else ssd_step_generic_kernel<T, GATE><<<grid, ((a.P + 63) / 64) * 64, 0, s>>>(a);
+    const bool vec = (a.N % 4 == 0) && ((uintptr_t)a.state % 16 == 0);
+    auto grid_for = [&](uint32_t NV) { return dim3(a.H * ((a.P + 256 / NV - 1) / (256 / NV)), a.batch); };
+    if (vec && nv == 32) ssd_step_kernel<T, 32, GATE><<<grid_for(32), 256, 0, s>>>(a);
+    else if (vec && nv == 16) ssd_step_kernel<T, 16, GATE><<<grid_for(16), 256, 0, s>>>(a);
+    else if (vec && nv == 64) ssd_step_kernel<T, 64, GATE><<<grid_for(64), 256, 0, s>>>(a);
+    else ssd_step_generic_kernel<T, GATE><<<dim3(a.H, a.batch), ((a.P + 63) / 64) * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
