@@ -33,6 +33,46 @@ def ssd_flops_per_token_head(Q=64, N=128, P=64):
     return 2 * Q * N + 2 * Q * P + 4 * N * P
 
 
+def inproj_args(L, m, sh, Lw, bufs):
+    """Arguments of one lssm_inproj_decode launch (batch 1) on layer weights Lw."""
+    hid, cst, zb, xb, db = bufs
+    return (hid.data_ptr(), Lw["norm_w"].data_ptr(), Lw["in_proj_w"].data_ptr(),
+            Lw["in_proj_s"].data_ptr(), cst.data_ptr(), Lw["conv1d_w"].data_ptr(),
+            Lw["conv1d_b"].data_ptr(), zb.data_ptr(), xb.data_ptr(), db.data_ptr(), 1,
+            sh.d_model, sh.d_inner, sh.d_state, sh.n_groups, sh.n_heads, sh.d_conv, 1e-5,
+            L.W_Q4_G64, L.BF16)
+
+
+def inproj_buffers(sh):
+    import torch
+    return (torch.randn(1, sh.d_model, device="cuda").to(torch.bfloat16),
+            torch.zeros(sh.xbc, sh.d_conv, dtype=torch.bfloat16, device="cuda"),
+            torch.empty(sh.d_inner, dtype=torch.bfloat16, device="cuda"),
+            torch.empty(sh.xbc, dtype=torch.bfloat16, device="cuda"),
+            torch.empty(sh.n_heads, dtype=torch.bfloat16, device="cuda"))
+
+
+def profile_kernel(L, ctx, m, sh, stream):
+    """Workload of the rocprofv3 --pmc runs: the dominant decode kernel over all
+    64 layers' weights, 10 times, then a 256 MiB device-to-device copy 10 times
+    (the known-size reference that scales the FETCH_SIZE / WRITE_SIZE counters)."""
+    import torch
+    bufs = inproj_buffers(sh)
+    args = [inproj_args(L, m, sh, Lw, bufs) for Lw in m.layers]
+    ctx.begin_batch()
+    for _ in range(10):
+        for a in args:
+            L.check(L.lib.lssm_inproj_decode(ctx.h, *a))
+    ctx.commit_and_wait()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_kernel": "inproj_decode", "launches": 10 * len(args),
+                      "copy_bytes": src.numel(), "copies": 10}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -46,6 +86,9 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only run the dominant decode kernel over all layers plus a 256 MiB "
+                         "device copy (the calibration reference for rocprofv3 --pmc runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -71,6 +114,9 @@ def main():
     print(f"[bench] model {args.model} built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     PB, PL = args.prefill_batch, args.prefill_len
     batches = [int(b) for b in args.batches.split(",") if b]
+    if args.profile_kernel:
+        profile_kernel(L, ctx, m, sh, stream)
+        return
     eng = Engine(ctx, m, max_batch=max([PB, 1] + batches), max_seq=PL)
 
     def timed(fn, reps=1):
@@ -128,21 +174,15 @@ def main():
         print(f"[bench] decode bs={b}: {tbt / n * 1e3:.3f} ms/step", file=sys.stderr, flush=True)
 
     # ---------------- dominant kernel, live (HIP events on the library's stream) ----------------
-    d_inner = sh.d_inner
-    hid = torch.randn(1, sh.d_model, device="cuda").to(torch.bfloat16)
-    cst = torch.zeros(sh.xbc, sh.d_conv, dtype=torch.bfloat16, device="cuda")
-    zb = torch.empty(d_inner, dtype=torch.bfloat16, device="cuda")
-    xb = torch.empty(sh.xbc, dtype=torch.bfloat16, device="cuda")
-    db = torch.empty(sh.n_heads, dtype=torch.bfloat16, device="cuda")
+    bufs = inproj_buffers(sh)
+    kargs = [inproj_args(L, m, sh, Lw, bufs) for Lw in m.layers]
+    fn = L.lib.lssm_inproj_decode
 
     def inproj_all_layers():
-        for Lw in m.layers:
-            L.check(L.lib.lssm_inproj_decode(
-                ctx.h, hid.data_ptr(), Lw["norm_w"].data_ptr(), Lw["in_proj_w"].data_ptr(),
-                Lw["in_proj_s"].data_ptr(), cst.data_ptr(), Lw["conv1d_w"].data_ptr(),
-                Lw["conv1d_b"].data_ptr(), zb.data_ptr(), xb.data_ptr(), db.data_ptr(), 1,
-                sh.d_model, d_inner, sh.d_state, sh.n_groups, sh.n_heads, sh.d_conv, 1e-5,
-                L.W_Q4_G64, L.BF16))
+        bad = 0
+        for a in kargs:
+            bad |= fn(ctx.h, *a)
+        L.check(bad)
 
     ctx.begin_batch()
     inproj_all_layers()
@@ -182,6 +222,13 @@ def main():
                          f"(C, OpenMP {nthr} threads)"}
         print(f"[bench] cpu oracle: {ct / args.cpu_steps:.2f} s/token", file=sys.stderr, flush=True)
 
+    # HBM bytes per launch of the same kernel from the two rocprofv3 --pmc passes
+    # (FETCH_SIZE, WRITE_SIZE, calibrated on a 256 MiB copy), recorded in profiles/
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "inproj_decode_traffic.json")
+    if args.model == "mamba2-2.7b" and os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("traffic_bytes")
+
     out = {
         "metric": "decode tok/s (bs=1) + prefill tok/s, Mamba-2-2.7B int4; % HBM/MFMA roofline",
         "value": round(tok_s, 2),
@@ -200,7 +247,7 @@ def main():
                    "layers": sh.n_layer, "d_model": sh.d_model, "vocab": sh.vocab_size,
                    "batch": 1, "prefill": f"{PB}x{PL}"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "inproj_decode (RMSNorm + in_proj int4-g64 GEMV + conv update + SiLU)",
                      "bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_us, 3)},
         "cpu_baseline": cpu,

@@ -120,10 +120,14 @@ const char* lssm_library_path(void);
 int lssm_kernel_count(void);
 const char* lssm_kernel_name(int i);
 
-/* Device memory plumbing (DeviceBuffer bodies, metal_buffer.mm:107-143). */
+/* Device memory plumbing (DeviceBuffer bodies, metal_buffer.mm:107-143).
+ * lssm_malloc: HBM.  lssm_malloc_host: pinned, coherent host memory that
+ * kernels read and write in place over PCIe (the shared-storage buffers of
+ * the reference's model layer); release it with lssm_free_host. */
 int lssm_malloc(void** out, size_t nbytes);
-int lssm_malloc_managed(void** out, size_t nbytes);
+int lssm_malloc_host(void** out, size_t nbytes);
 int lssm_free(void* p);
+int lssm_free_host(void* p);
 int lssm_memcpy_h2d(lssm_ctx* ctx, void* dst, const void* src, size_t nbytes);
 int lssm_memcpy_d2h(lssm_ctx* ctx, void* dst, const void* src, size_t nbytes);
 int lssm_memcpy_d2d(lssm_ctx* ctx, void* dst, const void* src, size_t nbytes);

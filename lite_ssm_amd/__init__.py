@@ -99,8 +99,9 @@ _SIGS = {
     "lssm_kernel_count": ([], _i),
     "lssm_kernel_name": ([_i], C.c_char_p),
     "lssm_malloc": ([C.POINTER(_vp), _sz], _i),
-    "lssm_malloc_managed": ([C.POINTER(_vp), _sz], _i),
+    "lssm_malloc_host": ([C.POINTER(_vp), _sz], _i),
     "lssm_free": ([_vp], _i),
+    "lssm_free_host": ([_vp], _i),
     "lssm_memcpy_h2d": ([_vp, _vp, _vp, _sz], _i),
     "lssm_memcpy_d2h": ([_vp, _vp, _vp, _sz], _i),
     "lssm_memcpy_d2d": ([_vp, _vp, _vp, _sz], _i),

@@ -212,14 +212,16 @@ int lssm_malloc(void** out, size_t nbytes) {
     return LSSM_OK;
 }
 
-int lssm_malloc_managed(void** out, size_t nbytes) {
+int lssm_malloc_host(void** out, size_t nbytes) {
     clear_error();
-    if (!out) return set_error(LSSM_EINVAL, "lssm_malloc_managed: null out");
+    if (!out) return set_error(LSSM_EINVAL, "lssm_malloc_host: null out");
     *out = nullptr;
     if (nbytes == 0) return LSSM_OK;
-    hipError_t e = hipMallocManaged(out, nbytes, hipMemAttachGlobal);
+    // Default flags: coherent, mapped into every device's address space, so
+    // the same pointer is used by host code and by kernels.
+    hipError_t e = hipHostMalloc(out, nbytes, hipHostMallocDefault);
     if (e != hipSuccess)
-        return set_error(LSSM_EDEVICE, "lssm_malloc_managed(%zu): %s", nbytes, hipGetErrorString(e));
+        return set_error(LSSM_EDEVICE, "lssm_malloc_host(%zu): %s", nbytes, hipGetErrorString(e));
     return LSSM_OK;
 }
 
@@ -228,6 +230,14 @@ int lssm_free(void* p) {
     if (!p) return LSSM_OK;
     hipError_t e = hipFree(p);
     if (e != hipSuccess) return set_error(LSSM_EDEVICE, "lssm_free: %s", hipGetErrorString(e));
+    return LSSM_OK;
+}
+
+int lssm_free_host(void* p) {
+    clear_error();
+    if (!p) return LSSM_OK;
+    hipError_t e = hipHostFree(p);
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "lssm_free_host: %s", hipGetErrorString(e));
     return LSSM_OK;
 }
 

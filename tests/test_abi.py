@@ -76,3 +76,50 @@ def test_oracle_library_is_separate_from_product():
     assert "oracle" not in out
     data = open(L.LIB_PATH, "rb").read()
     assert b"orc_model_decode" not in data
+
+
+# Methods of lite_ssm::MetalOps (reference include/lite_ssm/ops.hpp:60-240) and
+# of the buffer classes (include/lite_ssm/allocator.hpp:21-103).
+METALOPS_METHODS = [
+    "metallib_loaded", "has_pipeline", "metallib_path", "begin_batch", "commit_and_wait",
+    "batch_active", "rmsnorm_f16", "linear_f16_gemv", "linear_silu_f16_gemv",
+    "rmsnorm_linear_f16_gemv", "linear_f16_gemm", "linear_silu_f16_gemm", "linear_int4_gemv",
+    "linear_int4_gemm", "silu_f16", "add_inplace_f16", "split_silu_xBC_f16", "silu_gated_f16",
+    "causal_conv1d_f16", "causal_conv1d_update_f16", "seed_conv_state_f16", "inproj_fused_f16",
+    "ssd_chunked_f16", "ssd_step_f16",
+]
+
+
+def _demangled_exports(path):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "-C", "--defined-only", path], check=True,
+                         capture_output=True, text=True).stdout
+    return out
+
+
+def test_cpp_shim_exports_the_reference_interface():
+    path = os.path.join(ROOT, "lite_ssm_amd", "liblite_ssm_hip.so")
+    assert os.path.exists(path), "run __graft_entry__.build() first"
+    syms = re.sub(r"\[abi:\w+\]", "", _demangled_exports(path))
+    for m in METALOPS_METHODS:
+        assert f"lite_ssm::MetalOps::{m}(" in syms, m
+    for cls in ("MmapFile", "DeviceBuffer", "UnifiedBuffer"):
+        assert f"lite_ssm::{cls}::{cls}(" in syms, cls
+    assert "lite_ssm::DeviceBuffer::zero()" in syms
+    # every MetalOps method in the public header is one of these
+    hdr = open(os.path.join(ROOT, "include", "lite_ssm", "ops.hpp")).read()
+    declared = set(re.findall(r"^\s+(?:void|bool|const std::string&)\s+(\w+)\(", hdr, flags=re.M))
+    assert declared == set(METALOPS_METHODS)
+
+
+def test_cpp_metal_ops_test_skips_without_gpu():
+    """tests/cpp/test_metal_ops exits 77 (skip) when no GPU is present, like the
+    reference's test_metal_ops.cpp:20-27; on a GPU box it must pass (test_gpu_cpp)."""
+    import subprocess
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present: covered by tests/test_gpu_cpp.py")
+    exe = os.path.join(ROOT, "tests", "cpp", "_bin", "test_metal_ops")
+    assert os.path.exists(exe), "run __graft_entry__.build() first"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 77, r.stdout + r.stderr
