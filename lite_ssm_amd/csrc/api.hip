@@ -16,10 +16,10 @@ namespace {
 inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // GEMV fast-path requirements (gemv.hip): K a multiple of the 16-byte chunk,
-// 16-byte aligned weight rows, fp32 staging of <= 64 KiB per x row.
+// 16-byte aligned weight rows, one x row fits the fp32 LDS staging.
 bool gemv_ok(const void* w, uint32_t K, int wfmt, int act) {
     if (!al16(w)) return false;
-    if ((size_t)K * sizeof(float) > GEMV_LDS_BYTES) return false;
+    if (gemv_lds_rows(K, wfmt, act) < 1) return false;
     switch (wfmt) {
         case LSSM_W_Q4_B32: return K % 32 == 0;
         case LSSM_W_Q4_G64: return K % 64 == 0;

@@ -33,6 +33,13 @@ template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v
 template <typename T> __device__ __forceinline__ float rnd(float v) { return to_f(from_f<T>(v)); }
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+// SiLU with the hardware exp and reciprocal (about 1 ulp each): the reference
+// kernels are built with fast math (CMakeLists.txt:122), so this is within
+// their own rounding; used in decode epilogues where the full-precision
+// division is a measurable share of the instructions.
+__device__ __forceinline__ float silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+}
 __device__ __forceinline__ float softplus_f(float v) { return (v > 20.0f) ? v : logf(1.0f + expf(v)); }
 
 __device__ __forceinline__ float fp16_bits_to_f(uint16_t b) {

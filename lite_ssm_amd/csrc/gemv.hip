@@ -8,23 +8,25 @@
 // Two kernels, both reading every weight byte from HBM exactly once with
 // 16-byte loads (a "chunk": 32 int4 / 16 int8 / 8 dense weights of one row):
 //
-//  * gemv1 (M == 1, fp16 / bf16): LPR lanes own one row; lane l owns chunks
+//  * gemv1 (fp16 / bf16, M <= 4): LPR lanes own one row; lane l owns chunks
 //    l, l + LPR, ... (CPL of them), so the LPR lanes of a row cover all of K.
-//    The first row's weight chunks (and the epilogue's inputs) are issued
-//    before anything else; meanwhile the 512-thread block loads x once (one
-//    round of 16-byte loads of x and of the norm weight), RMSNorms it when
-//    fused, and stages it in LDS as packed pairs in the order the unpacked
-//    weights come out, with each chunk's sum(x) in the padding.  Waves then
-//    walk rows with the next row's chunks in flight while the current row is
-//    reduced.  Int4 / int8 are unpacked with mask-and-or "magic" constants into
-//    packed fp16 / bf16 pairs and multiplied with v_dot2 (exact products, fp32
-//    sums):
-//      fp16: ((q ^ 8) | 0x6400) = 1032 + q, then v_pk_add_f16 -1032 (exact);
-//      bf16: ((q ^ 8) | 0x4300) = 136 + q; 136 * sum(x) of the chunk is
-//            subtracted once per chunk.
+//    Every load of the kernel is issued first and unconditionally (indices
+//    clamped, scale and epilogue bits kept raw): the x rows and the norm
+//    weight, then the row's weight chunks, scales and epilogue inputs.  The
+//    256-thread block RMSNorms x (when fused) and stages it in LDS as packed
+//    pairs in the order the unpacked weights come out (plus each chunk's
+//    sum(x) where the unpack is biased) while the weights are in flight; each
+//    chunk is then unpacked once and multiplied with every x row (v_dot2:
+//    exact products, fp32 sums).  Unpacking:
+//      int4 x bf16: nibble ^ 8 as a byte, one v_perm per pair puts it under a
+//            0x43 byte: bf16 0x43XX = 136 + q; 136 * sum(x) is subtracted per chunk;
+//      int4 x fp16: ((q ^ 8) | 0x6400) = 1032 + q, then v_pk_add_f16 -1032 (exact);
+//      int8 x fp16: ((q ^ 128) | 0x6400) = 1152 + q, then -1152 (exact).
+//    Large N walks row groups with the next group's loads in flight
+//    (ping-pong register sets: no copies, so no early waits).
 //
-//  * gemv_lds (M <= 4, any dtype): x rows staged once per block in LDS as
-//    fp32, padded by 4 floats per chunk so that the 16-byte reads of the 16
+//  * gemv_lds (any dtype, any alignment): x rows staged once per block in LDS
+//    as fp32, padded by 4 floats per chunk so that the 16-byte reads of the 16
 //    lanes of a row fall in distinct banks; 16 lanes per row.
 #include "common.cuh"
 #include "internal.hpp"
@@ -38,11 +40,8 @@ typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GV_NT = 256;
-constexpr int G1_NT = 512;                       // gemv1 block: 8 waves share one x staging
+constexpr int G1_NT = 256;                       // smallest gemv1 block (4 waves)
 constexpr size_t GV_LDS_MAX = GEMV_LDS_BYTES;
-// LDS dwords per staged x chunk in gemv1: <= 16 packed pairs, the chunk's
-// sum(x), padding to 20 so that 16 lanes' 16-byte reads hit distinct banks.
-constexpr int GV_XS = 20;
 
 struct GemvCore {
     const void* x;
@@ -52,6 +51,7 @@ struct GemvCore {
     const void* norm_w;
     float eps;
     uint32_t N, K;
+    float inv_k;                                     // 1 / K (the RMSNorm mean)
 };
 
 template <int FMT, typename T> struct Fmt;
@@ -86,26 +86,51 @@ inline uint32_t wpc_of(int wfmt, int act) {
 // ---------------------------------------------------------------------------
 // Each epilogue has prefetch(m, n), issued together with the row's weight
 // loads, whose result is handed to operator() once the row's sum is ready.
-//
+// prefetch() loads unconditionally (clamped / substitute addresses) and keeps
+// raw bits: a conversion or a branch around a load would make the compiler
+// wait for it, and with it for every weight load issued before it.
+template <typename T> __device__ __forceinline__ uint32_t raw_at(const T* p) {
+    if constexpr (sizeof(T) == 2) return *reinterpret_cast<const uint16_t*>(p);
+    else return *reinterpret_cast<const uint32_t*>(p);
+}
+template <typename T> __device__ __forceinline__ float f_of_raw(uint32_t r) {
+    if constexpr (sizeof(T) == 2) return to_f(__builtin_bit_cast(T, (uint16_t)r));
+    else return __uint_as_float(r);
+}
+
+// Read a kernel argument into a register now (an empty asm that uses it):
+// pinned at kernel entry, no argument load is left for after the weight loads,
+// where it would queue behind the weight traffic.
+template <typename V> __device__ __forceinline__ void pin_arg(const V& v) {
+    if constexpr (sizeof(V) == 8) asm volatile("" ::"s"(v));
+    else asm volatile("" ::"s"(v));
+}
+
 // y[m, n] = r(acc) / r(silu(acc)) / r(res + r(acc))
 template <typename T> struct EpiPlain {
+    static constexpr bool kNormOptional = true;
     T* y;
     uint32_t y_stride;
     const T* res;
     int epi;
     struct Pre {
-        float r;
+        uint32_t r;
     };
+    __device__ __forceinline__ void pin() const {
+        pin_arg(y);
+        pin_arg(y_stride);
+        pin_arg(res);
+        pin_arg(epi);
+    }
     __device__ __forceinline__ Pre prefetch(int m, uint32_t n) const {
-        Pre p{0.0f};
-        if (epi == LSSM_EPI_ADD) p.r = to_f(res[(size_t)m * y_stride + n]);
-        return p;
+        const T* src = (epi == LSSM_EPI_ADD) ? res : y;   // y: a valid address, value unused
+        return Pre{raw_at(src + ((uint32_t)m * y_stride + n))};
     }
     __device__ __forceinline__ void operator()(int m, uint32_t n, float acc, const Pre& p) const {
         const size_t i = (size_t)m * y_stride + n;
         float v = acc;
         if (epi == LSSM_EPI_SILU) v = silu_f(acc);
-        else if (epi == LSSM_EPI_ADD) v = p.r + rnd<T>(acc);
+        else if (epi == LSSM_EPI_ADD) v = f_of_raw<T>(p.r) + rnd<T>(acc);
         y[i] = from_f<T>(v);
     }
 };
@@ -115,6 +140,7 @@ template <typename T> struct EpiPlain {
 // -> xbc_act, remaining rows -> dt.  The pre-conv xBC value is r(acc), the conv
 // output is rounded once more before SiLU, as in the unfused op sequence.
 template <typename T> struct EpiInproj {
+    static constexpr bool kNormOptional = false;           // always behind the layer RMSNorm
     uint32_t d_inner, xbc, H, dconv;
     T* conv_state;
     const T* conv_w;
@@ -125,16 +151,34 @@ template <typename T> struct EpiInproj {
     // the 4-tap window, weights and bias of an xBC row (2-byte T, d_conv == 4)
     struct Pre {
         uint2 s, w;
-        float b;
+        uint32_t b;
     };
     static constexpr bool kVec = sizeof(T) == 2;
+    __device__ __forceinline__ void pin() const {
+        pin_arg(d_inner);
+        pin_arg(xbc);
+        pin_arg(H);
+        pin_arg(dconv);
+        pin_arg(conv_state);
+        pin_arg(conv_w);
+        pin_arg(conv_b);
+        pin_arg(z);
+        pin_arg(xbc_act);
+        pin_arg(dt);
+    }
     __device__ __forceinline__ Pre prefetch(int m, uint32_t n) const {
-        Pre p{make_uint2(0, 0), make_uint2(0, 0), 0.0f};
-        if (kVec && dconv == 4 && n >= d_inner && n < d_inner + xbc) {
-            const uint32_t c = n - d_inner;
-            p.s = *reinterpret_cast<const uint2*>(conv_state + ((size_t)m * xbc + c) * 4);
-            p.w = *reinterpret_cast<const uint2*>(conv_w + (size_t)c * 4);
-            p.b = to_f(conv_b[c]);
+        Pre p{make_uint2(0, 0), make_uint2(0, 0), 0u};
+        if constexpr (kVec) {
+            // clamped channel; element 0 when the window is not 4 wide (value unused)
+            uint32_t c = n < d_inner ? 0u : n - d_inner;
+            c = c < xbc ? c : xbc - 1;
+            c = dconv == 4 ? c : 0u;
+            // 32-bit offsets: 64-bit multiply-adds here get register pairs whose
+            // high half is a pending load, which forces a wait for every load
+            const uint32_t so = ((uint32_t)m * xbc + c) * dconv, wo = c * dconv;
+            p.s = *reinterpret_cast<const uint2*>(conv_state + so);
+            p.w = *reinterpret_cast<const uint2*>(conv_w + wo);
+            p.b = raw_at(conv_b + c);
         }
         return p;
     }
@@ -152,8 +196,8 @@ template <typename T> struct EpiInproj {
                     const T* s = reinterpret_cast<const T*>(&p.s);
                     const T* w = reinterpret_cast<const T*>(&p.w);
                     // window shift (conv1d.metal:127-130): taps 1..3 move down, x lands in 3
-                    a = p.b + to_f(s[1]) * to_f(w[0]) + to_f(s[2]) * to_f(w[1]) + to_f(s[3]) * to_f(w[2]) +
-                        to_f(v) * to_f(w[3]);
+                    a = f_of_raw<T>(p.b) + to_f(s[1]) * to_f(w[0]) + to_f(s[2]) * to_f(w[1]) +
+                        to_f(s[3]) * to_f(w[2]) + to_f(v) * to_f(w[3]);
                     uint2 ns;
                     ns.x = p.s.x >> 16 | p.s.y << 16;                                     // (s1, s2)
                     ns.y = p.s.y >> 16 | (uint32_t)__builtin_bit_cast(uint16_t, v) << 16;  // (s3, x)
@@ -172,7 +216,7 @@ template <typename T> struct EpiInproj {
                 sd[dconv - 1] = v;
                 a += to_f(v) * to_f(wd[dconv - 1]);
             }
-            xbc_act[(size_t)m * xbc + c] = from_f<T>(silu_f(rnd<T>(a)));
+            xbc_act[(size_t)m * xbc + c] = from_f<T>(silu_fast(rnd<T>(a)));
         } else {
             dt[(size_t)m * H + (n - d_inner - xbc)] = v;
         }
@@ -180,7 +224,7 @@ template <typename T> struct EpiInproj {
 };
 
 // ---------------------------------------------------------------------------
-// gemv1: M == 1, x in registers
+// gemv1: M <= 4 rows of x staged once per block as packed pairs
 // ---------------------------------------------------------------------------
 template <typename T> __device__ __forceinline__ uint32_t bits16(T v) {
     return (uint32_t)__builtin_bit_cast(uint16_t, v);
@@ -200,12 +244,28 @@ __device__ __forceinline__ uint32_t pk_add_f16(uint32_t a, float c) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+template <int FMT> constexpr bool is_q4() { return FMT == LSSM_W_Q4_B32 || FMT == LSSM_W_Q4_G64; }
+// int4 x bf16: byte-select unpack, q + 136 per weight, 136 * sum(x) subtracted per chunk
+template <int FMT, typename T> constexpr bool q4_bf16() { return is_q4<FMT>() && __is_same(T, bf16); }
+
+// LDS dwords per staged x chunk: the packed pairs, the chunk's sum(x) when the
+// unpack is biased, padding so that the 16-byte reads of consecutive lanes
+// (consecutive chunks) fall in distinct banks.
+template <int NP> constexpr int xs_of() { return NP == 4 ? 4 : NP == 8 ? 12 : 20; }
+
 // Position (within the chunk) of the two x values paired with packed pair p.
-// Q4: dword i, pair j (shift 4j) holds weights 8i+j and 8i+j+4.
-// Q8: dword i holds weights 4i..4i+3; pair 0 = (4i, 4i+2), pair 1 = (4i+1, 4i+3).
-// Dense: natural pairs (2p, 2p+1).
-template <int FMT> __device__ __forceinline__ void pair_pos(int p, int& a, int& b) {
-    if constexpr (FMT == LSSM_W_Q4_B32 || FMT == LSSM_W_Q4_G64) {
+//  int4 x bf16: dword i gives lo = nibbles (0, 2, 4, 6), hi = (1, 3, 5, 7) of
+//    its 8 weights 8i..8i+7 as bytes; pairs (lo.b0, lo.b1), (lo.b2, lo.b3),
+//    (hi.b0, hi.b1), (hi.b2, hi.b3) = weights (0,2), (4,6), (1,3), (5,7).
+//  int4 x f16: dword i, pair j (shift 4j) holds weights 8i+j and 8i+j+4.
+//  int8: dword i holds weights 4i..4i+3; pair 0 = (4i, 4i+2), pair 1 = (4i+1, 4i+3).
+//  dense: natural pairs (2p, 2p+1).
+template <int FMT, typename T> __device__ __forceinline__ void pair_pos(int p, int& a, int& b) {
+    if constexpr (q4_bf16<FMT, T>()) {
+        const int i = p / 4, j = p % 4;
+        a = 8 * i + ((j & 2) ? 1 : 0) + ((j & 1) ? 4 : 0);
+        b = a + 2;
+    } else if constexpr (is_q4<FMT>()) {
         a = 8 * (p / 4) + (p % 4);
         b = a + 4;
     } else if constexpr (FMT == LSSM_W_Q8_G32) {
@@ -217,161 +277,266 @@ template <int FMT> __device__ __forceinline__ void pair_pos(int p, int& a, int& 
     }
 }
 
-// sum_pairs dot of one weight chunk with the packed x pairs xp[0..WPC/2).
+// One 16-byte weight chunk unpacked into packed fp16 / bf16 pairs.
+template <int FMT, typename T> struct Unpacked {
+    static constexpr int NP = Fmt<FMT, T>::WPC / 2;
+    uint32_t p[NP];
+};
 template <int FMT, typename T>
-__device__ __forceinline__ float chunk_dot2(const uint4 wv, const uint32_t* xp) {
+__device__ __forceinline__ Unpacked<FMT, T> unpack(const uint4 wv) {
     const uint32_t d[4] = {wv.x, wv.y, wv.z, wv.w};
-    float acc = 0.0f;
-    if constexpr (FMT == LSSM_W_Q4_B32 || FMT == LSSM_W_Q4_G64) {
+    Unpacked<FMT, T> u;
+    if constexpr (q4_bf16<FMT, T>()) {
+        // q + 8 per nibble, as bytes; v_perm puts each byte under a 0x43 byte:
+        // bf16 0x43XX = 128 + XX
+        constexpr uint32_t MAGIC = 0x43434343u;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t u = d[i] ^ 0x88888888u;            // nibble -> q + 8
+            const uint32_t lo = (d[i] ^ 0x08080808u) & 0x0F0F0F0Fu;
+            const uint32_t hi = ((d[i] >> 4) ^ 0x08080808u) & 0x0F0F0F0Fu;
+            u.p[4 * i + 0] = __builtin_amdgcn_perm(MAGIC, lo, 0x04010400u);
+            u.p[4 * i + 1] = __builtin_amdgcn_perm(MAGIC, lo, 0x04030402u);
+            u.p[4 * i + 2] = __builtin_amdgcn_perm(MAGIC, hi, 0x04010400u);
+            u.p[4 * i + 3] = __builtin_amdgcn_perm(MAGIC, hi, 0x04030402u);
+        }
+    } else if constexpr (is_q4<FMT>()) {
+        // fp16 0x64XX = 1024 + XX; - 1032 is exact
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t m = (u >> (4 * j)) & 0x000F000Fu;
-                if constexpr (sizeof(T) == 2 && __is_same(T, f16)) {
-                    const uint32_t h = pk_add_f16(m | 0x64006400u, -1032.0f);   // exact q
-                    acc = dot2(h, xp[4 * i + j], acc, f16{});
-                } else {
-                    acc = dot2(m | 0x43004300u, xp[4 * i + j], acc, bf16{});    // q + 136
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t v = d[i] ^ 0x88888888u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) u.p[4 * i + j] = pk_add_f16(((v >> (4 * j)) & 0x000F000Fu) | 0x64006400u, -1032.0f);
         }
     } else if constexpr (FMT == LSSM_W_Q8_G32) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t u = d[i] ^ 0x80808080u;            // byte -> q + 128
-            const uint32_t h0 = pk_add_f16((u & 0x00FF00FFu) | 0x64006400u, -1152.0f);
-            const uint32_t h1 = pk_add_f16(((u >> 8) & 0x00FF00FFu) | 0x64006400u, -1152.0f);
-            acc = dot2(h0, xp[2 * i], acc, f16{});
-            acc = dot2(h1, xp[2 * i + 1], acc, f16{});
+            const uint32_t v = d[i] ^ 0x80808080u;            // byte -> q + 128
+            u.p[2 * i] = pk_add_f16((v & 0x00FF00FFu) | 0x64006400u, -1152.0f);
+            u.p[2 * i + 1] = pk_add_f16(((v >> 8) & 0x00FF00FFu) | 0x64006400u, -1152.0f);
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc = dot2(d[i], xp[i], acc, T{});
+        for (int i = 0; i < 4; ++i) u.p[i] = d[i];
     }
-    return acc;
+    return u;
 }
 
-template <int FMT, typename T, int LPR, int CPL, bool NORM, class Epi>
-__global__ __launch_bounds__(G1_NT) void gemv1_kernel(GemvCore c, Epi epi) {
+// Weights, raw scale bits and epilogue inputs of the rows one wave handles.
+template <int CPL, int MR, class Epi> struct RowSet {
+    uint4 wq[CPL];
+    uint16_t sc[CPL];
+    typename Epi::Pre pre[MR];
+    uint32_t n;
+};
+
+template <int FMT, typename T, int LPR, int CPL, int OCT, int MR, bool NORM, bool LOOP, int NTMAX, class Epi>
+__global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint32_t iters, int mr) {
     using F = Fmt<FMT, T>;
     constexpr int WPC = F::WPC;
     constexpr int NP = WPC / 2;                      // packed pairs per chunk
-    constexpr int RPW = WAVE / LPR;                  // rows per wave per step
-    constexpr bool BIAS136 = (FMT == LSSM_W_Q4_B32 || FMT == LSSM_W_Q4_G64) && !__is_same(T, f16);
-    extern __shared__ uint32_t xl[];                 // [cpr][XS]: NP packed pairs, sum(x), pad
-    __shared__ float red[G1_NT / WAVE];
+    constexpr int XS = xs_of<NP>();
+    constexpr int RPW = WAVE / LPR;                  // rows per wave
+    constexpr bool BIAS = q4_bf16<FMT, T>();
+    constexpr uint32_t GD = F::G ? F::G : 1;
+    extern __shared__ uint32_t xl[];                 // [MR][cpr][XS]
+    __shared__ float red[MR][NTMAX / WAVE];
+    const uint32_t BD = blockDim.x;                  // >= G1_NT, a multiple of the wave
+    const uint32_t NWB = BD / WAVE;
     const int lane = threadIdx.x % WAVE;
     const int lr = lane % LPR;
+    const uint32_t wbase = threadIdx.x & ~(uint32_t)(WAVE - 1);
     const uint32_t K = c.K;
-    const uint32_t nwaves = gridDim.x * (G1_NT / WAVE);
-    const uint32_t ngroups = (c.N + RPW - 1) / RPW;
+    const uint32_t cpr = K / WPC;
+    const uint32_t noct = K / 8;
     const size_t rb = F::row_bytes(K);
-    constexpr uint32_t GD = F::G ? F::G : 1;
     const uint32_t gpr = K / GD;
 
-    auto load = [&](uint32_t n, uint4* wq, float* sc) {
-        if (n < c.N) {
-            const uint8_t* wr = c.w + (size_t)n * rb;
+    pin_arg(c.x);
+    pin_arg(c.x_stride);
+    pin_arg(c.w);
+    pin_arg(c.s);
+    pin_arg(c.norm_w);
+    pin_arg(c.eps);
+    pin_arg(c.N);
+    pin_arg(c.K);
+    pin_arg(c.inv_k);
+    epi.pin();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 1. x rows and the norm weight, requested before any weight ----
+    // A CU's vector loads return in request order, so the block issues all its
+    // x loads, meets at a barrier that waits for no memory, and only then asks
+    // for its weights: x is not queued behind the weight traffic.
+    uint4 xo[MR][OCT], wo[OCT];
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const uint32_t ch = lr + LPR * j;
-                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (size_t)ch * 16));
-                wq[j] = make_uint4(v[0], v[1], v[2], v[3]);
-                if constexpr (F::G > 0) sc[j] = fp16_bits_to_f(c.s[(size_t)n * gpr + (ch * WPC) / GD]);
-                else sc[j] = 1.0f;
+    for (int i = 0; i < OCT; ++i) {
+        if (wbase + BD * i < noct) {                 // wave-uniform
+            uint32_t o = threadIdx.x + BD * i;
+            o = o < noct ? o : noct - 1;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const int mc = m < mr ? m : mr - 1;      // rows past mr: a duplicate, never stored
+                xo[m][i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(c.x) + (size_t)mc * c.x_stride + 8 * o);
             }
+            if constexpr (NORM) wo[i] = reinterpret_cast<const uint4*>(c.norm_w)[o];
         }
+    }
+    // ---- 2. scales and epilogue inputs of the first row set, then weights ----
+    // The small loads (a 2-byte scale per chunk, the epilogue's inputs) go out
+    // here, while the memory system is quiet: issued behind the weights they
+    // would hold the wave as long as the weight traffic pushes back.  The
+    // 16-byte weight chunks are requested after the last barrier.  Scheduling
+    // barriers pin the issue order; waits count loads in issue order.
+    const uint32_t nwaves = gridDim.x * NWB;
+    const uint32_t wv = blockIdx.x * NWB + threadIdx.x / WAVE;
+    auto load_side = [&](RowSet<CPL, MR, Epi>& rs, uint32_t group) {
+        rs.n = group * RPW + lane / LPR;
+        const uint32_t nc = rs.n < c.N ? rs.n : c.N - 1;   // clamped: every lane loads
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (F::G > 0) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) rs.sc[j] = c.s[(size_t)nc * gpr + ((lr + LPR * j) * WPC) / GD];
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) rs.pre[m] = epi.prefetch(m < mr ? m : mr - 1, nc);
+        __builtin_amdgcn_sched_barrier(0);
     };
-
-    // ---- 1. the first row's weight chunks (and epilogue inputs) go out first ----
-    uint32_t rg = blockIdx.x * (G1_NT / WAVE) + threadIdx.x / WAVE;
-    uint32_t n = rg * RPW + lane / LPR;
-    uint4 wq[CPL];
-    float sc[CPL];
-    typename Epi::Pre pre{};
-    if (rg < ngroups) {
-        load(n, wq, sc);
-        if (lr == 0 && n < c.N) pre = epi.prefetch(0, n);
-    }
-
-    // ---- 2. stage x (RMSNorm'ed when fused, norm.metal:52-79) as packed pairs ----
-    // Thread t owns octets (8 consecutive x) t, t + NT, ...: one round of 16-byte
-    // loads of x and of the norm weight, a block reduction, then packing.
-    constexpr int OCT = 4;                           // octets per thread: K <= 8 * NT * OCT
-    const uint4* x4 = reinterpret_cast<const uint4*>(c.x);
-    const uint4* nw4 = reinterpret_cast<const uint4*>(c.norm_w);
-    const uint32_t noct = K / 8;
-    uint4 xo[OCT], wo[OCT];
-    float ss = 0.0f;
+    auto load_w = [&](RowSet<CPL, MR, Epi>& rs) {
+        const uint32_t nc = rs.n < c.N ? rs.n : c.N - 1;
+        const uint8_t* wr = c.w + (size_t)nc * rb;
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < OCT; ++i) {
-        const uint32_t o = threadIdx.x + G1_NT * i;
-        if (o < noct) {
-            xo[i] = x4[o];
-            if constexpr (NORM) wo[i] = nw4[o];
-            const T* t = reinterpret_cast<const T*>(&xo[i]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float v = to_f(t[e]);
-                ss += v * v;
-            }
+        for (int j = 0; j < CPL; ++j) {
+            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (size_t)(lr + LPR * j) * 16));
+            rs.wq[j] = make_uint4(v[0], v[1], v[2], v[3]);
         }
-    }
-    float rrms = 1.0f;
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    RowSet<CPL, MR, Epi> A;
+    load_side(A, wv);
+
+    // ---- 1b. sum(x^2) and 1/rms, finished before any weight is requested ----
+    // Requested together with the weights, x queues behind the whole chip's
+    // weight misses in L2 (~2.5 us); alone it returns in well under 1 us, and
+    // normalising and staging then overlap the weight stream.  sum(x^2) uses
+    // v_dot2 on packed pairs (exact products, fp32 sums).
+    float rr[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) rr[m] = 1.0f;
     if constexpr (NORM) {
-        ss = block_sum<G1_NT>(ss, red);
-        rrms = 1.0f / sqrtf(ss / (float)K + c.eps);
-    }
+        float ss[MR];
 #pragma unroll
-    for (int i = 0; i < OCT; ++i) {
-        const uint32_t o = threadIdx.x + G1_NT * i;       // uniform in i across a wave's lanes
-        if (G1_NT * i >= noct) break;
-        float v[8];
-        float s = 0.0f;
-        if (o < noct) {
-            const T* t = reinterpret_cast<const T*>(&xo[i]);
-            const T* tw = reinterpret_cast<const T*>(&wo[i]);
+        for (int m = 0; m < MR; ++m) ss[m] = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                v[e] = to_f(t[e]);
-                if constexpr (NORM) v[e] = rnd<T>(v[e] * to_f(tw[e]) * rrms);
-                s += v[e];
-            }
-            const uint32_t k0 = o * 8, ch = k0 / WPC, off = k0 % WPC;
-            uint32_t* dst = xl + (size_t)ch * GV_XS;
+        for (int i = 0; i < OCT; ++i) {
+            if (wbase + BD * i >= noct) break;
+            const bool live = threadIdx.x + BD * i < noct;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                int a, b;
-                pair_pos<FMT>((int)(off / 2) + q, a, b);
-                dst[off / 2 + q] = pack2<T>(v[a - (int)off], v[b - (int)off]);
+            for (int m = 0; m < MR; ++m) {
+                const uint4 d = xo[m][i];
+                float q = dot2(d.x, d.x, 0.0f, T{});
+                q = dot2(d.y, d.y, q, T{});
+                q = dot2(d.z, d.z, q, T{});
+                q = dot2(d.w, d.w, q, T{});
+                ss[m] += live ? q : 0.0f;
             }
         }
-        // sum(x) of a chunk: its WPC/8 octets sit in consecutive lanes
-        s = group_sum<WPC / 8>(s);
-        if (o < noct && (o % (WPC / 8)) == 0) xl[(size_t)(o * 8 / WPC) * GV_XS + NP] = __float_as_uint(s);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) ss[m] = wave_sum(ss[m]);
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) red[m][threadIdx.x / WAVE] = ss[m];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float t = 0.0f;
+            for (uint32_t w = 0; w < NWB; ++w) t += red[m][w];
+            rr[m] = rsqrtf(t * c.inv_k + c.eps);
+        }
+    } else {
+        // no norm: the block meets once its x loads are issued (no wait)
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
-    if (rg >= ngroups) return;
 
-    // ---- 3. rows: next row's chunks in flight while this one is reduced ----
-    for (;;) {
-        const uint32_t rg_next = rg + nwaves;
-        const bool more = rg_next < ngroups;
-        const uint32_t n_next = rg_next * RPW + lane / LPR;
-        uint4 wq2[CPL];
-        float sc2[CPL];
-        typename Epi::Pre pre2{};
-        if (more) {
-            load(n_next, wq2, sc2);
-            if (lr == 0 && n_next < c.N) pre2 = epi.prefetch(0, n_next);
-        }
-        float acc = 0.0f;
-        if (n < c.N) {
+
+    // ---- 3. stage x (RMSNorm'ed when fused, norm.metal:52-79) as packed pairs ----
+    // Only the waves holding x octets stage (a wave-uniform branch).  The
+    // normalised values are rounded straight into the pairs; the chunk sums
+    // use v_dot2 with (1, 1).
+    {
+        constexpr uint32_t ONES = __is_same(T, f16) ? 0x3C003C00u : 0x3F803F80u;   // (1, 1)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const uint32_t* src = xl + (size_t)(lr + LPR * j) * GV_XS;
+        for (int i = 0; i < OCT; ++i) {
+            if (wbase + BD * i >= noct) break;
+            const uint32_t o = threadIdx.x + BD * i;
+            const uint32_t k0 = o * 8, ch = k0 / WPC, off = k0 % WPC;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const T* t = reinterpret_cast<const T*>(&xo[m][i]);
+                float v[8];
+                if constexpr (NORM) {
+                    // x * w exactly (v_dot2 of a pair with one half of the other
+                    // pair masked), then * 1/rms: the fp32 products of the reference
+                    const uint32_t* xd = reinterpret_cast<const uint32_t*>(&xo[m][i]);
+                    const uint32_t* wd = reinterpret_cast<const uint32_t*>(&wo[i]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] = dot2(xd[e], wd[e] & 0x0000FFFFu, 0.0f, T{}) * rr[m];
+                        v[2 * e + 1] = dot2(xd[e], wd[e] & 0xFFFF0000u, 0.0f, T{}) * rr[m];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = to_f(t[e]);
+                }
+                uint4 pk;
+                uint32_t* pq = reinterpret_cast<uint32_t*>(&pk);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    int a, b;
+                    pair_pos<FMT, T>((int)(off / 2) + q, a, b);
+                    pq[q] = pack2<T>(v[a - (int)off], v[b - (int)off]);   // the rounding r()
+                }
+                uint32_t* dst = xl + ((size_t)m * cpr + ch) * XS;
+                if (o < noct) *reinterpret_cast<uint4*>(dst + off / 2) = pk;
+                if constexpr (BIAS) {
+                    // sum(x) of a chunk: its WPC/8 octets sit in consecutive lanes
+                    float s = dot2(pq[0], ONES, 0.0f, T{});
+                    s = dot2(pq[1], ONES, s, T{});
+                    s = dot2(pq[2], ONES, s, T{});
+                    s = dot2(pq[3], ONES, s, T{});
+                    s = group_sum<WPC / 8>(s);
+                    if (o < noct && (o % (WPC / 8)) == 0) dst[NP] = __float_as_uint(s);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Weights are requested after the last barrier: a wave issuing loads is
+    // held for as long as the memory system pushes back, and no barrier may
+    // wait on that.
+    load_w(A);
+
+
+    // ---- 4. rows; the next row's loads are in flight while this one is reduced ----
+    auto compute = [&](const RowSet<CPL, MR, Epi>& rs) {
+        float acc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const Unpacked<FMT, T> u = unpack<FMT, T>(rs.wq[j]);
+            float sc = 1.0f;
+            if constexpr (F::G > 0) sc = fp16_bits_to_f(rs.sc[j]);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const uint32_t* src = xl + ((size_t)m * cpr + lr + LPR * j) * XS;
                 uint32_t xp[NP];
 #pragma unroll
                 for (int q = 0; q < NP / 4; ++q) {
@@ -381,56 +546,156 @@ __global__ __launch_bounds__(G1_NT) void gemv1_kernel(GemvCore c, Epi epi) {
                     xp[4 * q + 2] = v.z;
                     xp[4 * q + 3] = v.w;
                 }
-                float d = chunk_dot2<FMT, T>(wq[j], xp);
-                if constexpr (BIAS136) d -= 136.0f * __uint_as_float(src[NP]);
-                acc += d * sc[j];
+                float d = 0.0f;
+#pragma unroll
+                for (int q = 0; q < NP; ++q) d = dot2(u.p[q], xp[q], d, T{});
+                if constexpr (BIAS) d -= 136.0f * __uint_as_float(src[NP]);
+                acc[m] += d * sc;
             }
         }
-        acc = group_sum<LPR>(acc);
-        if (lr == 0 && n < c.N) epi(0, n, acc, pre);
-        if (!more) break;
-        rg = rg_next;
-        n = n_next;
-        pre = pre2;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            wq[j] = wq2[j];
-            sc[j] = sc2[j];
+        for (int m = 0; m < MR; ++m) {
+            const float a = group_sum<LPR>(acc[m]);
+            if (lr == 0 && rs.n < c.N && m < mr) epi(m, rs.n, a, rs.pre[m]);
+        }
+    };
+    if constexpr (!LOOP) {
+        compute(A);
+    } else {
+        // ping-pong between two row sets: no register copies, so no early waits
+        RowSet<CPL, MR, Epi> B;
+        for (uint32_t it = 0; it < iters; it += 2) {
+            if (it + 1 < iters) {
+                load_side(B, wv + (it + 1) * nwaves);
+                load_w(B);
+            }
+            compute(A);
+            if (it + 1 >= iters) break;
+            if (it + 2 < iters) {
+                load_side(A, wv + (it + 2) * nwaves);
+                load_w(A);
+            }
+            compute(B);
         }
     }
 }
 
-
-template <int FMT, typename T, int LPR, int CPL, class Epi>
-hipError_t go1(hipStream_t s, const GemvCore& c, const Epi& e, int norm) {
-    constexpr int RPW = WAVE / LPR;
-    const uint32_t ngroups = (c.N + RPW - 1) / RPW;
-    uint32_t waves = ngroups < 3072u ? ngroups : 3072u;     // ~3 resident waves per SIMD
-    const uint32_t blocks = (waves + (G1_NT / WAVE) - 1) / (G1_NT / WAVE);
-    const size_t lds = (size_t)(c.K / Fmt<FMT, T>::WPC) * GV_XS * sizeof(uint32_t);
-    if (norm) gemv1_kernel<FMT, T, LPR, CPL, true, Epi><<<blocks, G1_NT, lds, s>>>(c, e);
-    else gemv1_kernel<FMT, T, LPR, CPL, false, Epi><<<blocks, G1_NT, lds, s>>>(c, e);
-    return hipGetLastError();
+// Compute units of the current device (queried once per process).
+inline uint32_t num_cus() {
+    static const uint32_t n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return 256u;
+        return (uint32_t)cus;
+    }();
+    return n;
 }
 
-// (lanes per row, chunks per lane) for the chunk counts of the model shapes.
-template <int FMT, typename T, class Epi>
-hipError_t launch_gemv1(hipStream_t s, const GemvCore& c, const Epi& e, int norm, bool& done) {
+template <int FMT, typename T, int LPR, int CPL, int MR, class Epi>
+hipError_t go1(hipStream_t s, const GemvCore& c, const Epi& e, int mr, int norm) {
+    constexpr int RPW = WAVE / LPR;
+    constexpr int NW = G1_NT / WAVE;
+    using F = Fmt<FMT, T>;
+    constexpr uint32_t KC = (uint32_t)LPR * CPL * F::WPC;     // the K this shape is built for
+    constexpr int OCT = (int)((KC / 8 + G1_NT - 1) / G1_NT);
+    static_assert(OCT >= 1 && OCT <= 4, "x staging: K <= 8192");
+    // Dense single-row GEMVs (the lm_head, N up to 256k) walk row groups with
+    // a bounded grid, so that x is staged by few blocks.  Otherwise every wave
+    // takes one row group and single-row launches size their blocks to put
+    // one block on each CU (x staged once per CU, requested ahead of the
+    // CU's weight traffic); multi-row launches (high register use) keep
+    // 256-thread blocks.
+    constexpr bool LOOP = FMT == LSSM_W_DENSE && MR == 1;
+    constexpr int NTMAX = MR == 1 ? 1024 : G1_NT;
+    const uint32_t ngroups = (c.N + RPW - 1) / RPW;
+    const uint32_t cap = 4096;                                 // 4 resident waves per SIMD
+    const uint32_t iters = LOOP ? (ngroups + cap - 1) / cap : 1u;
+    const uint32_t waves = (ngroups + iters - 1) / iters;
+    uint32_t wpb = NW;                                         // waves per block
+    if (MR == 1) {
+        const uint32_t per_cu = (waves + num_cus() - 1) / num_cus();
+        wpb = per_cu < (uint32_t)NW ? (uint32_t)NW : per_cu > 16u ? 16u : per_cu;
+    }
+    const uint32_t blocks = (waves + wpb - 1) / wpb;
+    const size_t lds = (size_t)MR * (KC / F::WPC) * xs_of<F::WPC / 2>() * sizeof(uint32_t);
+    if (c.K != KC || lds > GV_LDS_MAX) return hipErrorInvalidValue;
+    auto run = [&](auto k) -> hipError_t {
+        // opt in to the full dynamic LDS once per instantiation (a host attribute)
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)GV_LDS_MAX);
+        if (attr != hipSuccess) return attr;
+        k<<<blocks, wpb * WAVE, lds, s>>>(c, e, iters, mr);
+        return hipGetLastError();
+    };
+    if (norm) return run(gemv1_kernel<FMT, T, LPR, CPL, OCT, MR, true, LOOP, NTMAX, Epi>);
+    if constexpr (Epi::kNormOptional) return run(gemv1_kernel<FMT, T, LPR, CPL, OCT, MR, false, LOOP, NTMAX, Epi>);
+    return hipErrorInvalidValue;
+}
+
+// (lanes per row, chunks per lane) for the chunk counts of the model shapes
+// (d_model / d_inner of 130M, 2.7B, 8B and 2048), per weight format.
+template <int FMT, typename T, int MR, class Epi>
+hipError_t launch_gemv1(hipStream_t s, const GemvCore& c, const Epi& e, int mr, int norm, bool& done) {
     done = true;
     const uint32_t cpr = c.K / Fmt<FMT, T>::WPC;
-    switch (cpr) {
-        case 48: return go1<FMT, T, 16, 3, Epi>(s, c, e, norm);
-        case 64: return go1<FMT, T, 16, 4, Epi>(s, c, e, norm);
-        case 80: return go1<FMT, T, 16, 5, Epi>(s, c, e, norm);
-        case 96: return go1<FMT, T, 32, 3, Epi>(s, c, e, norm);
-        case 128: return go1<FMT, T, 32, 4, Epi>(s, c, e, norm);
-        case 160: return go1<FMT, T, 32, 5, Epi>(s, c, e, norm);
-        case 192: return go1<FMT, T, 64, 3, Epi>(s, c, e, norm);
-        case 256: return go1<FMT, T, 64, 4, Epi>(s, c, e, norm);
-        case 320: return go1<FMT, T, 64, 5, Epi>(s, c, e, norm);
-        case 512: return go1<FMT, T, 64, 8, Epi>(s, c, e, norm);
-        default: done = false; return hipSuccess;
+    if constexpr (is_q4<FMT>()) {                             // K = 1536 .. 8192
+        switch (cpr) {
+            case 48: return go1<FMT, T, 16, 3, MR, Epi>(s, c, e, mr, norm);
+            case 64: return go1<FMT, T, 16, 4, MR, Epi>(s, c, e, mr, norm);
+            case 80: return go1<FMT, T, 16, 5, MR, Epi>(s, c, e, mr, norm);
+            case 128: return go1<FMT, T, 32, 4, MR, Epi>(s, c, e, mr, norm);
+            case 160: return go1<FMT, T, 32, 5, MR, Epi>(s, c, e, mr, norm);
+            case 256: return go1<FMT, T, 64, 4, MR, Epi>(s, c, e, mr, norm);
+        }
+    } else if constexpr (FMT == LSSM_W_Q8_G32) {              // K = 768 .. 8192
+        switch (cpr) {
+            case 48: return go1<FMT, T, 16, 3, MR, Epi>(s, c, e, mr, norm);
+            case 96: return go1<FMT, T, 32, 3, MR, Epi>(s, c, e, mr, norm);
+            case 128: return go1<FMT, T, 32, 4, MR, Epi>(s, c, e, mr, norm);
+            case 160: return go1<FMT, T, 32, 5, MR, Epi>(s, c, e, mr, norm);
+            case 256: return go1<FMT, T, 64, 4, MR, Epi>(s, c, e, mr, norm);
+            case 320: return go1<FMT, T, 64, 5, MR, Epi>(s, c, e, mr, norm);
+            case 512: return go1<FMT, T, 64, 8, MR, Epi>(s, c, e, mr, norm);
+        }
+    } else {                                                  // dense, K = 768 .. 4096
+        switch (cpr) {
+            case 96: return go1<FMT, T, 32, 3, MR, Epi>(s, c, e, mr, norm);
+            case 192: return go1<FMT, T, 64, 3, MR, Epi>(s, c, e, mr, norm);
+            case 256: return go1<FMT, T, 64, 4, MR, Epi>(s, c, e, mr, norm);
+            case 320: return go1<FMT, T, 64, 5, MR, Epi>(s, c, e, mr, norm);
+            case 512: return go1<FMT, T, 64, 8, MR, Epi>(s, c, e, mr, norm);
+        }
     }
+    done = false;
+    return hipSuccess;
+}
+
+template <int FMT> bool gemv1_shape(uint32_t cpr) {
+    if constexpr (is_q4<FMT>()) return cpr == 48 || cpr == 64 || cpr == 80 || cpr == 128 || cpr == 160 || cpr == 256;
+    else if constexpr (FMT == LSSM_W_Q8_G32)
+        return cpr == 48 || cpr == 96 || cpr == 128 || cpr == 160 || cpr == 256 || cpr == 320 || cpr == 512;
+    else return cpr == 96 || cpr == 192 || cpr == 256 || cpr == 320 || cpr == 512;
+}
+
+// Largest MR the gemv1 staging of this K / format fits (0 = not a gemv1 shape).
+inline int gemv1_rows(uint32_t K, int wfmt, int act) {
+    if (act == LSSM_F32 || (wfmt == LSSM_W_Q8_G32 && act != LSSM_F16)) return 0;
+    const uint32_t wpc = wpc_of(wfmt, act);
+    if (K % wpc != 0) return 0;
+    const uint32_t cpr = K / wpc;
+    bool ok;
+    switch (wfmt) {
+        case LSSM_W_Q4_B32:
+        case LSSM_W_Q4_G64: ok = gemv1_shape<LSSM_W_Q4_G64>(cpr); break;
+        case LSSM_W_Q8_G32: ok = gemv1_shape<LSSM_W_Q8_G32>(cpr); break;
+        default: ok = gemv1_shape<LSSM_W_DENSE>(cpr); break;
+    }
+    if (!ok) return 0;
+    const uint32_t np = wpc / 2;
+    const size_t per_row = (size_t)cpr * (np == 4 ? 4 : np == 8 ? 12 : 20) * sizeof(uint32_t);
+    const int mr = (int)(GV_LDS_MAX / per_row);
+    return mr > 4 ? 4 : mr;
 }
 
 // ---------------------------------------------------------------------------
@@ -565,26 +830,58 @@ hipError_t launch_lds_mr(hipStream_t s, const GemvCore& c, const Epi& e, int mr,
     }
 }
 
-// Format dispatch: M == 1 on fp16/bf16 tries gemv1 first.
+// Largest number of x rows per launch whose padded fp32 LDS staging fits.
+inline int lds_rows(uint32_t K, int wfmt, int act) {
+    const uint32_t wpc = wpc_of(wfmt, act);
+    int mr = (int)(GV_LDS_MAX / ((size_t)padded_len(K, wpc) * sizeof(float)));
+    return mr > 4 ? 4 : mr;
+}
+
+template <typename T> constexpr int act_of() {
+    return __is_same(T, f16) ? LSSM_F16 : __is_same(T, bf16) ? LSSM_BF16 : LSSM_F32;
+}
+
+// Rows of x one launch of this call can take: gemv1 when its 16-byte loads
+// are aligned and the shape is one of its table, else the fp32 LDS kernel.
+template <typename T> int rows_for(const GemvCore& c, int wfmt, int norm) {
+    const bool aligned = ((uintptr_t)c.x % 16 == 0) && ((c.x_stride * sizeof(T)) % 16 == 0) &&
+                         (!norm || (uintptr_t)c.norm_w % 16 == 0) && ((uintptr_t)c.w % 16 == 0);
+    const int g1 = aligned ? gemv1_rows(c.K, wfmt, act_of<T>()) : 0;
+    return g1 > 0 ? g1 : lds_rows(c.K, wfmt, act_of<T>());
+}
+
+// MR in {1, 2, 4}; three rows run in the four-row kernel (a duplicate row, not stored).
+template <int FMT, typename T, class Epi>
+hipError_t launch_gemv1_mr(hipStream_t s, const GemvCore& c, const Epi& e, int mr, int norm, bool& done) {
+    switch (mr) {
+        case 1: return launch_gemv1<FMT, T, 1, Epi>(s, c, e, mr, norm, done);
+        case 2: return launch_gemv1<FMT, T, 2, Epi>(s, c, e, mr, norm, done);
+        default: return launch_gemv1<FMT, T, 4, Epi>(s, c, e, mr, norm, done);
+    }
+}
+
+// Format dispatch: fp16 / bf16 with aligned operands go to gemv1.
 template <typename T, class Epi>
 hipError_t launch_fmt(hipStream_t s, const GemvCore& c, const Epi& e, int mr, int wfmt, int norm) {
-    const bool aligned = ((uintptr_t)c.x % 16 == 0) && (!norm || (uintptr_t)c.norm_w % 16 == 0) &&
-                         ((uintptr_t)c.w % 16 == 0);
+    if (mr < 1 || mr > rows_for<T>(c, wfmt, norm)) return hipErrorInvalidValue;
     if constexpr (!__is_same(T, float)) {
-      if (mr == 1 && aligned) {
-        bool done = false;
-        hipError_t err = hipSuccess;
-        switch (wfmt) {
-            case LSSM_W_Q4_B32: err = launch_gemv1<LSSM_W_Q4_B32, T, Epi>(s, c, e, norm, done); break;
-            case LSSM_W_Q4_G64: err = launch_gemv1<LSSM_W_Q4_G64, T, Epi>(s, c, e, norm, done); break;
-            case LSSM_W_Q8_G32:
-                if constexpr (__is_same(T, f16)) err = launch_gemv1<LSSM_W_Q8_G32, T, Epi>(s, c, e, norm, done);
-                break;
-            default: err = launch_gemv1<LSSM_W_DENSE, T, Epi>(s, c, e, norm, done); break;
+        const bool aligned = ((uintptr_t)c.x % 16 == 0) && ((c.x_stride * sizeof(T)) % 16 == 0) &&
+                             (!norm || (uintptr_t)c.norm_w % 16 == 0) && ((uintptr_t)c.w % 16 == 0);
+        if (aligned && gemv1_rows(c.K, wfmt, act_of<T>()) >= mr) {
+            bool done = false;
+            hipError_t err = hipSuccess;
+            switch (wfmt) {
+                case LSSM_W_Q4_B32: err = launch_gemv1_mr<LSSM_W_Q4_B32, T, Epi>(s, c, e, mr, norm, done); break;
+                case LSSM_W_Q4_G64: err = launch_gemv1_mr<LSSM_W_Q4_G64, T, Epi>(s, c, e, mr, norm, done); break;
+                case LSSM_W_Q8_G32:
+                    if constexpr (__is_same(T, f16)) err = launch_gemv1_mr<LSSM_W_Q8_G32, T, Epi>(s, c, e, mr, norm, done);
+                    break;
+                default: err = launch_gemv1_mr<LSSM_W_DENSE, T, Epi>(s, c, e, mr, norm, done); break;
+            }
+            if (done) return err;
         }
-        if (done) return err;
-      }
     }
+    if (mr > lds_rows(c.K, wfmt, act_of<T>())) return hipErrorInvalidValue;
     switch (wfmt) {
         case LSSM_W_Q4_B32: return launch_lds_mr<LSSM_W_Q4_B32, T, Epi>(s, c, e, mr, norm);
         case LSSM_W_Q4_G64: return launch_lds_mr<LSSM_W_Q4_G64, T, Epi>(s, c, e, mr, norm);
@@ -593,22 +890,23 @@ hipError_t launch_fmt(hipStream_t s, const GemvCore& c, const Epi& e, int mr, in
     }
 }
 
-// Largest number of x rows per launch whose padded fp32 LDS staging fits.
+// Rows per launch when operands are aligned (what callers plan with).
 inline int max_rows(uint32_t K, int wfmt, int act) {
-    const uint32_t wpc = wpc_of(wfmt, act);
-    int mr = (int)(GV_LDS_MAX / ((size_t)padded_len(K, wpc) * sizeof(float)));
-    return mr > 4 ? 4 : mr;
+    const int g1 = gemv1_rows(K, wfmt, act);
+    const int l = lds_rows(K, wfmt, act);
+    return g1 > l ? g1 : l;
 }
 
 template <typename T>
 hipError_t gemv_plain(hipStream_t s, const GemvArgs& a) {
     const size_t es = sizeof(T);
-    const int mrmax = max_rows(a.K, a.wfmt, a.act);
+    GemvCore c0{a.x, a.x_stride, (const uint8_t*)a.w, (const uint16_t*)a.s, a.norm_w, a.eps, a.N, a.K, 1.0f / (float)a.K};
+    const int mrmax = rows_for<T>(c0, a.wfmt, a.norm_w ? 1 : 0);
     if (mrmax < 1) return hipErrorInvalidValue;
     for (uint32_t m0 = 0; m0 < a.M; m0 += (uint32_t)mrmax) {
         const int mr = (int)((a.M - m0) < (uint32_t)mrmax ? (a.M - m0) : (uint32_t)mrmax);
         GemvCore c{(const char*)a.x + (size_t)m0 * a.x_stride * es, a.x_stride,
-                   (const uint8_t*)a.w, (const uint16_t*)a.s, a.norm_w, a.eps, a.N, a.K};
+                   (const uint8_t*)a.w, (const uint16_t*)a.s, a.norm_w, a.eps, a.N, a.K, 1.0f / (float)a.K};
         EpiPlain<T> e{(T*)a.y + (size_t)m0 * a.y_stride, a.y_stride,
                       a.res ? (const T*)a.res + (size_t)m0 * a.y_stride : nullptr, a.epi};
         hipError_t err = launch_fmt<T>(s, c, e, mr, a.wfmt, a.norm_w ? 1 : 0);
@@ -639,6 +937,7 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, const uint16_t* __
 }  // namespace
 
 int gemv_max_rows(uint32_t K, int wfmt, int act) { return max_rows(K, wfmt, act); }
+int gemv_lds_rows(uint32_t K, int wfmt, int act) { return lds_rows(K, wfmt, act); }
 
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a) {
     if (a.M == 0 || a.N == 0) return hipSuccess;
@@ -650,8 +949,7 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a) {
 hipError_t launch_inproj_decode(hipStream_t s, const InprojDecodeArgs& a) {
     const GemvArgs& g = a.g;
     if (g.M == 0) return hipSuccess;
-    if ((int)g.M > max_rows(g.K, g.wfmt, g.act)) return hipErrorInvalidValue;
-    GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K};
+    GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
     auto go = [&](auto tag) -> hipError_t {
         using T = decltype(tag);
         EpiInproj<T> e{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,

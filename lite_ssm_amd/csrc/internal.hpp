@@ -103,8 +103,10 @@ struct GemvArgs {
     int wfmt, act, epi;
 };
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a);
-// Rows of x one GEMV launch can stage in LDS for this K / format (0 = none).
+// Rows of x one GEMV launch can take for this K / format (0 = none), with
+// 16-byte aligned operands / with any alignment.
 int gemv_max_rows(uint32_t K, int wfmt, int act);
+int gemv_lds_rows(uint32_t K, int wfmt, int act);
 hipError_t launch_dequant(hipStream_t s, const void* w, const void* sc, float* out, uint32_t N,
                           uint32_t K, int wfmt);
 

@@ -19,49 +19,78 @@ namespace lssm {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Decode step.  Block (h * PS + ps, b), 256 threads, owns RB = 256 / (N/4)
-// rows p of one head's (P, N) fp32 state; each thread streams exactly one
-// float4 of state (one 16-byte load and store), so all of a block's loads are
-// independent and in flight together.  The N/4 lanes of a row reduce C.s with
-// shuffles.  P is spread over PS blocks to put H * PS * batch blocks on the
-// 256 CUs (bs=1, 2.7B: 640 blocks).
+// Decode step.  Block (h * PS + ps, b), 256 threads, owns 32 rows p of one
+// head's (P, N) fp32 state: 8 lanes per row, each streaming F = N / 32 float4
+// of state.  Every load is issued first and unconditionally (state, the
+// lane's B and C vectors, then the per-row / per-head scalars as raw bits), so
+// nothing waits before the math; the 8 lanes of a row reduce C.s with
+// shuffles.  2.7B at batch 1: 160 blocks, 4 x 16-byte state loads per thread.
 // ---------------------------------------------------------------------------
-template <typename T, int NV, bool GATE>
+constexpr int ST_NV = 8;                              // lanes per state row
+constexpr int ST_RB = 256 / ST_NV;                    // rows per block
+
+template <typename T> __device__ __forceinline__ uint32_t raw_of(const T* p) {
+    if constexpr (sizeof(T) == 2) return *reinterpret_cast<const uint16_t*>(p);
+    else return *reinterpret_cast<const uint32_t*>(p);
+}
+template <typename T> __device__ __forceinline__ float f_of(uint32_t r) {
+    if constexpr (sizeof(T) == 2) return to_f(__builtin_bit_cast(T, (uint16_t)r));
+    else return __uint_as_float(r);
+}
+
+template <typename T, int F, bool GATE>
 __global__ __launch_bounds__(256) void ssd_step_kernel(SsdArgs a) {
-    constexpr uint32_t RB = 256 / NV;
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
     const uint32_t P = a.P, N = a.N;
-    const uint32_t PS = (P + RB - 1) / RB;
+    const uint32_t PS = (P + ST_RB - 1) / ST_RB;
     const uint32_t h = blockIdx.x / PS, ps = blockIdx.x % PS, b = blockIdx.y;
-    const uint32_t p = ps * RB + threadIdx.x / NV;
-    if (p >= P) return;                               // whole NV-lane row groups exit together
-    const uint32_t hpg = (a.H / a.G) > 0 ? a.H / a.G : 1;
-    const uint32_t g = h / hpg;
-    const uint32_t lr = threadIdx.x % NV;             // float4 column within the row
-    const uint32_t n = lr * 4;
-    float4* S = reinterpret_cast<float4*>(a.state + (((size_t)b * a.H + h) * P + p) * N) + lr;
-    float4 s = *S;
-    const T* Bv = (const T*)a.B + (size_t)b * a.b_stride + (size_t)g * N + n;
-    const T* Cv = (const T*)a.C + (size_t)b * a.c_stride + (size_t)g * N + n;
-    const float xv = to_f(((const T*)a.X)[(size_t)b * a.x_stride + (size_t)h * P + p]);
-    const float A_h = -expf(to_f(((const T*)a.A_log)[h]));
-    float dt = softplus_f(to_f(((const T*)a.dt)[(size_t)b * a.dt_stride + h]) + to_f(((const T*)a.dt_bias)[h]));
+    const uint32_t p = ps * ST_RB + threadIdx.x / ST_NV;
+    if (p >= P) return;                               // whole 8-lane row groups exit together
+    const uint32_t g = h / (a.H / a.G);
+    const uint32_t lr = threadIdx.x % ST_NV;
+    f32x4* S = reinterpret_cast<f32x4*>(a.state + (((size_t)b * a.H + h) * P + p) * N);
+    const T4* B4 = reinterpret_cast<const T4*>((const T*)a.B + (size_t)b * a.b_stride + (size_t)g * N);
+    const T4* C4 = reinterpret_cast<const T4*>((const T*)a.C + (size_t)b * a.c_stride + (size_t)g * N);
+    f32x4 s[F];
+    T4 bv[F], cv[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) s[f] = S[lr + ST_NV * f];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        bv[f] = B4[lr + ST_NV * f];
+        cv[f] = C4[lr + ST_NV * f];
+    }
+    const T* Xp = (const T*)a.X + (size_t)b * a.x_stride + (size_t)h * P + p;
+    const uint32_t xr = raw_of(Xp);
+    const uint32_t zr = GATE ? raw_of((const T*)a.z + (size_t)b * a.z_stride + (size_t)h * P + p) : 0u;
+    const uint32_t alr = raw_of((const T*)a.A_log + h);
+    const uint32_t dtr = raw_of((const T*)a.dt + (size_t)b * a.dt_stride + h);
+    const uint32_t dbr = raw_of((const T*)a.dt_bias + h);
+    const uint32_t dr = raw_of(a.has_D ? (const T*)a.D + h : Xp);   // value unused without D
+
+    // dt = clamp(softplus(dt_raw + dt_bias)), decay = e^{A dt} (ssd_step.metal:55-66)
+    const float xv = f_of<T>(xr);
+    const float A_h = -expf(f_of<T>(alr));
+    float dt = softplus_f(f_of<T>(dtr) + f_of<T>(dbr));
     dt = fminf(fmaxf(dt, a.dt_min), a.dt_max);
     const float decay = expf(A_h * dt);
-    const float D_h = a.has_D ? to_f(((const T*)a.D)[h]) : 0.0f;
-    // s = decay*s + (dt*B)*x  (ssd_step.metal:68-69)
-    s.x = decay * s.x + dt * to_f(Bv[0]) * xv;
-    s.y = decay * s.y + dt * to_f(Bv[1]) * xv;
-    s.z = decay * s.z + dt * to_f(Bv[2]) * xv;
-    s.w = decay * s.w + dt * to_f(Bv[3]) * xv;
-    *S = s;
-    float ys = to_f(Cv[0]) * s.x + to_f(Cv[1]) * s.y + to_f(Cv[2]) * s.z + to_f(Cv[3]) * s.w;
-    ys = group_sum<NV>(ys);
+    float ys = 0.0f;
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        // s = decay*s + (dt*B)*x  (ssd_step.metal:68-69)
+        f32x4 t = s[f];
+        t.x = decay * t.x + dt * to_f(bv[f].x) * xv;
+        t.y = decay * t.y + dt * to_f(bv[f].y) * xv;
+        t.z = decay * t.z + dt * to_f(bv[f].z) * xv;
+        t.w = decay * t.w + dt * to_f(bv[f].w) * xv;
+        S[lr + ST_NV * f] = t;
+        ys += to_f(cv[f].x) * t.x + to_f(cv[f].y) * t.y + to_f(cv[f].z) * t.z + to_f(cv[f].w) * t.w;
+    }
+    ys = group_sum<ST_NV>(ys);
     if (lr == 0) {
-        float y = rnd<T>(ys + D_h * xv);
-        if constexpr (GATE) {
-            const T* Z = (const T*)a.z + (size_t)b * a.z_stride + (size_t)h * P;
-            y = silu_f(to_f(Z[p])) * y;
-        }
+        float y = rnd<T>(ys + (a.has_D ? f_of<T>(dr) : 0.0f) * xv);
+        if constexpr (GATE) y = silu_fast(f_of<T>(zr)) * y;
         ((T*)a.Y)[(size_t)b * a.y_stride + (size_t)h * P + p] = from_f<T>(y);
     }
 }
@@ -418,12 +447,15 @@ __global__ __launch_bounds__(MF_NT) void ssd_chunk_mfma_kernel(SsdArgs a) {
 
 template <typename T, bool GATE>
 hipError_t step_go(hipStream_t s, const SsdArgs& a) {
-    const uint32_t nv = a.N / 4;
-    const bool vec = (a.N % 4 == 0) && ((uintptr_t)a.state % 16 == 0);
-    auto grid_for = [&](uint32_t NV) { return dim3(a.H * ((a.P + 256 / NV - 1) / (256 / NV)), a.batch); };
-    if (vec && nv == 32) ssd_step_kernel<T, 32, GATE><<<grid_for(32), 256, 0, s>>>(a);
-    else if (vec && nv == 16) ssd_step_kernel<T, 16, GATE><<<grid_for(16), 256, 0, s>>>(a);
-    else if (vec && nv == 64) ssd_step_kernel<T, 64, GATE><<<grid_for(64), 256, 0, s>>>(a);
+    // vector path: 4-element B / C vectors aligned, fp32 state 16-byte aligned
+    const size_t v4 = 4 * sizeof(T);
+    const bool vec = ((uintptr_t)a.state % 16 == 0) && ((uintptr_t)a.B % v4 == 0) &&
+                     ((uintptr_t)a.C % v4 == 0) && (a.b_stride % 4 == 0) && (a.c_stride % 4 == 0);
+    const dim3 grid(a.H * ((a.P + ST_RB - 1) / ST_RB), a.batch);
+    if (vec && a.N == 128) ssd_step_kernel<T, 4, GATE><<<grid, 256, 0, s>>>(a);
+    else if (vec && a.N == 64) ssd_step_kernel<T, 2, GATE><<<grid, 256, 0, s>>>(a);
+    else if (vec && a.N == 256) ssd_step_kernel<T, 8, GATE><<<grid, 256, 0, s>>>(a);
+    else if (vec && a.N == 32) ssd_step_kernel<T, 1, GATE><<<grid, 256, 0, s>>>(a);
     else ssd_step_generic_kernel<T, GATE><<<dim3(a.H, a.batch), ((a.P + 63) / 64) * 64, 0, s>>>(a);
     return hipGetLastError();
 }
