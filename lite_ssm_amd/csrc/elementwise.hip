@@ -127,6 +127,74 @@ __global__ void conv1d_kernel(const T* __restrict__ x, uint32_t xs, const T* __r
     y[(row0 + t) * ys + d] = from_f<T>(o);
 }
 
+// Vector form of conv1d_kernel for 2-byte dtypes and K == 4: a thread owns 8
+// consecutive channels (16-byte loads and stores) and CT consecutive time
+// steps, with the CT + 3 input rows it needs held in registers, so every
+// input row is read once per thread (not once per tap) and the taps and
+// bias once per thread.  Same sums in the same order as conv1d_kernel.
+constexpr int CONV_CT = 16;
+
+template <typename T, bool SILU>
+__global__ __launch_bounds__(256) void conv1d_vec_kernel(const T* __restrict__ x, uint32_t xs,
+                                                         const T* __restrict__ w,
+                                                         const T* __restrict__ bias,
+                                                         T* __restrict__ y, uint32_t ys, uint32_t L,
+                                                         uint32_t D) {
+  if constexpr (sizeof(T) == 2) {                    // launched for fp16 / bf16 only
+    const uint32_t d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (d0 >= D) return;
+    const uint32_t t0 = blockIdx.y * CONV_CT;
+    const uint32_t b = blockIdx.z;
+    const T* xb = x + (size_t)b * L * xs + d0;
+    uint4 win[CONV_CT + 3];
+#pragma unroll
+    for (int i = 0; i < CONV_CT + 3; ++i) {
+        const int t = (int)t0 + i - 3;
+        win[i] = (t >= 0 && t < (int)L) ? *reinterpret_cast<const uint4*>(xb + (size_t)t * xs)
+                                        : make_uint4(0, 0, 0, 0);
+    }
+    // taps w[d][0..3] of the 8 channels: 64 contiguous bytes
+    float wf[8][4], bf[8];
+    {
+        const uint4* w4 = reinterpret_cast<const uint4*>(w + (size_t)d0 * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = w4[q];
+            const T* tv = reinterpret_cast<const T*>(&v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wf[2 * q + e / 4][e % 4] = to_f(tv[e]);
+        }
+        if (bias) {
+            const uint4 v = *reinterpret_cast<const uint4*>(bias + d0);
+            const T* tv = reinterpret_cast<const T*>(&v);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) bf[c] = to_f(tv[c]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) bf[c] = 0.0f;
+        }
+    }
+    T* yb = y + ((size_t)b * L + t0) * ys + d0;
+#pragma unroll
+    for (int i = 0; i < CONV_CT; ++i) {
+        if (t0 + i >= L) break;
+        uint4 out;
+        T* ov = reinterpret_cast<T*>(&out);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float acc = bf[c];
+#pragma unroll
+            for (int tap = 0; tap < 4; ++tap)
+                acc += wf[c][tap] * to_f(reinterpret_cast<const T*>(&win[i + tap])[c]);
+            float o = rnd<T>(acc);
+            if (SILU) o = silu_f(o);
+            ov[c] = from_f<T>(o);
+        }
+        *reinterpret_cast<uint4*>(yb + (size_t)i * ys) = out;
+    }
+  }
+}
+
 // conv1d.metal:108-137 — shift the window left, append x, y = r(bias + sum s*w).
 template <typename T>
 __global__ void conv1d_update_kernel(const T* __restrict__ x_new, T* state, const T* __restrict__ w,
@@ -325,6 +393,22 @@ hipError_t launch_conv1d(hipStream_t s, const void* x, uint32_t xs, const void* 
                          void* y, uint32_t ys, uint32_t B, uint32_t L, uint32_t D, uint32_t K,
                          int act, bool silu) {
     if ((size_t)B * L * D == 0) return hipSuccess;
+    const bool vec = act != LSSM_F32 && K == 4 && D % 8 == 0 && xs % 8 == 0 && ys % 8 == 0 &&
+                     (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)w % 16 == 0 &&
+                     (bias == nullptr || (uintptr_t)bias % 16 == 0);
+    if (vec) {
+        dim3 gv(cdiv(D / 8, 256), cdiv(L, CONV_CT), B);
+        if (silu) {
+            LSSM_DISPATCH_ACT(act, T,
+                              conv1d_vec_kernel<T, true><<<gv, 256, 0, s>>>((const T*)x, xs, (const T*)w,
+                                                                            (const T*)bias, (T*)y, ys, L, D));
+        } else {
+            LSSM_DISPATCH_ACT(act, T,
+                              conv1d_vec_kernel<T, false><<<gv, 256, 0, s>>>((const T*)x, xs, (const T*)w,
+                                                                             (const T*)bias, (T*)y, ys, L, D));
+        }
+        return hipGetLastError();
+    }
     dim3 grid(cdiv(D, NT), L, B);
     if (silu) {
         LSSM_DISPATCH_ACT(act, T,
