@@ -42,6 +42,18 @@ int finish(lssm_ctx* ctx, const char* what) {
 
 __global__ void lite_ssm_common_noop() {}
 
+// Compute units of the current device (queried once per process).
+uint32_t num_cus() {
+    static const uint32_t n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return 256u;
+        return (uint32_t)cus;
+    }();
+    return n;
+}
+
 }  // namespace lssm
 
 using namespace lssm;

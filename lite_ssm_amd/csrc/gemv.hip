@@ -580,18 +580,6 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
     }
 }
 
-// Compute units of the current device (queried once per process).
-inline uint32_t num_cus() {
-    static const uint32_t n = [] {
-        int dev = 0, cus = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            return 256u;
-        return (uint32_t)cus;
-    }();
-    return n;
-}
-
 template <int FMT, typename T, int LPR, int CPL, int MR, class Epi>
 hipError_t go1(hipStream_t s, const GemvCore& c, const Epi& e, int mr, int norm) {
     constexpr int RPW = WAVE / LPR;

@@ -24,6 +24,9 @@ struct lssm_ctx {
 
 namespace lssm {
 
+// Compute units of the current device (queried once per process).
+uint32_t num_cus();
+
 // thread-local error message (lssm_last_error)
 int set_error(int code, const char* fmt, ...);
 void clear_error();

@@ -221,228 +221,335 @@ __global__ __launch_bounds__(SC_NT) void ssd_chunk_scalar_kernel(SsdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Chunked scan on MFMA (fp16 / bf16), chunk = 64, N = 128, P % 32 == 0.
-// Block (h * P/32 + pb, b), 256 threads = 4 waves, owns 32 columns of P.
-// Per chunk, with v_mfma_f32_16x16x32 (lane l: A row l%16 / B column l%16,
-// k = (l/16)*8 .. +8; D element r at row (l/16)*4 + r, column l%16):
-//   G  = C_c . B_c^T          [64 x 64]  K = 128   (wave w: rows 16w..16w+15)
-//   M  = r(G o decay o DT) -> LDS
-//   Y  = M . X_c + e^{Lcum} (C_c . S^T) + D x     [64 x 32]
-//   S  = r(e^{L_end} S + (X_c o w)^T . B_c)        [32 x 128], fp32 in registers
-// The rounded S is also kept in LDS as the B operand of the next C_c . S^T.
+// Chunked scan on MFMA (fp16 / bf16), chunk Q = 64, N = 128, P % (16 NW) == 0.
+// Block (h * P/(16 NW) + pb, b), NW waves; wave w owns the 16 state columns
+// p = 16 w .. +16 of the block's slice.  v_mfma_f32_16x16x32 operand lanes:
+// lane l = 16 q + i supplies row/column i and k = 8 q .. 8 q + 7; the result
+// holds rows 4 q .. 4 q + 3 of column i.  All products put the token index on
+// k, so token-major tiles (B, X) are read with the gfx950 LDS transpose load
+// (ds_read_b64_tr_b16: lane i of each 16-lane group gets column i of the
+// four rows read by lane blocks 0..3).  Per chunk:
+//   G^T[j][t] = B_j . C_t                    (10 lower tiles, shared by the waves)
+//   M[t][j]   = r(G^T e^{Lc_t - Lc_j} DT_j)  -> LDS, token-major
+//   Y^T[p][t] = X^T M^T + e^{Lc_t} (S . C_t) + D x      (wave: 16 p x 64 t)
+//   S^T[n][p] = r(e^{L_end} S^T + B^T (w o X)),  w_j = e^{L_end - Lc_j} DT_j
+// S^T lives in registers as fp32 (the rounded values), laid out so that its
+// tiles are directly the k = n operand of S . C_t.  The next chunk's B, C, X
+// and dt are prefetched into registers during the current chunk; two
+// barriers per chunk.
 // ---------------------------------------------------------------------------
-constexpr int MF_NT = 256;
-constexpr int MF_Q = 64;      // chunk
-constexpr int MF_N = 128;     // state size
-constexpr int MF_PB = 32;     // P columns per block
-constexpr int NPAD = MF_N + 8;
-constexpr int QPAD = MF_Q + 8;
+constexpr int CQ = 64;            // chunk
+constexpr int CN = 128;           // state size
+constexpr int SPAD = CN + 8;      // B / C row pitch (elements)
+constexpr int MPAD = CQ + 8;      // M row pitch
 
-template <typename T> struct Mfma16;
-template <> struct Mfma16<f16> {
-    using frag = half8;
-    static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-};
-template <> struct Mfma16<bf16> {
-    using frag = bf16x8;
-    static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-};
+typedef short s4v __attribute__((ext_vector_type(4)));
+typedef short s8v __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <typename T>
-__global__ __launch_bounds__(MF_NT) void ssd_chunk_mfma_kernel(SsdArgs a) {
-    __shared__ __attribute__((aligned(16))) T Cc[MF_Q * NPAD];
-    __shared__ __attribute__((aligned(16))) T Bc[MF_Q * NPAD];
-    __shared__ __attribute__((aligned(16))) T Sl[MF_PB * NPAD];
-    __shared__ __attribute__((aligned(16))) T Xt[MF_PB * QPAD];
-    __shared__ __attribute__((aligned(16))) T Ml[MF_Q * QPAD];
-    __shared__ float DT[MF_Q], Lc[MF_Q];
-    using Op = Mfma16<T>;
-    using frag = typename Op::frag;
+template <typename T> __device__ __forceinline__ floatx4 mma16(s8v a, s8v b, floatx4 c) {
+    if constexpr (__is_same(T, bf16))
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
+                                                      __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+
+// Transposed 64-bit LDS load (see above); p must be 8-byte aligned.
+__device__ __forceinline__ s4v ld_tr(const void* p) {
+    typedef __attribute__((address_space(3))) s4v lds_s4v;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v*)(const_cast<void*>(p)));
+}
+
+template <typename T> __device__ __forceinline__ short bits_of(float v) {
+    return __builtin_bit_cast(short, from_f<T>(v));
+}
+template <typename T> __device__ __forceinline__ float val_of(short v) {
+    return to_f(__builtin_bit_cast(T, v));
+}
+template <typename T> __device__ __forceinline__ s4v pack4(floatx4 v) {
+    s4v r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = bits_of<T>(v[e]);
+    return r;
+}
+__device__ __forceinline__ s8v cat8(s4v lo, s4v hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <typename T> __device__ __forceinline__ floatx4 unpack4(s4v v) {
+    floatx4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = val_of<T>(v[e]);
+    return r;
+}
+
+template <typename T, int NW>
+__global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
+    constexpr int NT = 64 * NW;           // threads
+    constexpr int PB = 16 * NW;           // state columns p per block
+    constexpr int XP = PB + 8;            // X row pitch
+    constexpr int BV = CQ * CN / 8 / NT;  // 16-byte pieces of B (and of C) per thread
+    constexpr int XV = CQ * PB / 8 / NT;  // 16-byte pieces of X per thread (= 2)
+    constexpr int BR = NT / 16;           // B / C rows per load round
+    constexpr int XR = NT / (PB / 8);     // X rows per load round
+    __shared__ __attribute__((aligned(16))) T Bs[CQ * SPAD];
+    __shared__ __attribute__((aligned(16))) T Cs[CQ * SPAD];
+    __shared__ __attribute__((aligned(16))) T Xs[CQ * XP];
+    __shared__ __attribute__((aligned(16))) T Ms[CQ * MPAD];
+    // per-token chunk scalars, double-buffered: wave 0 computes chunk c + 1's
+    // while the block works on chunk c
+    __shared__ __attribute__((aligned(16))) float LCb[2][CQ], DTb[2][CQ], ELb[2][CQ], Wb[2][CQ];
 
     const uint32_t P = a.P, H = a.H, L = a.L;
-    const uint32_t npb = P / MF_PB;
+    const uint32_t npb = P / PB;
     const uint32_t h = blockIdx.x / npb, pb = blockIdx.x % npb, b = blockIdx.y;
-    const uint32_t p0 = pb * MF_PB;
+    const uint32_t p0 = pb * PB;
     const uint32_t hpg = (H / a.G) > 0 ? H / a.G : 1;
     const uint32_t g = h / hpg;
     const T* X = (const T*)a.X + (size_t)b * L * a.x_stride + (size_t)h * P + p0;
-    const T* Bv = (const T*)a.B + (size_t)b * L * a.b_stride + (size_t)g * MF_N;
-    const T* Cv = (const T*)a.C + (size_t)b * L * a.c_stride + (size_t)g * MF_N;
+    const T* Bv = (const T*)a.B + (size_t)b * L * a.b_stride + (size_t)g * CN;
+    const T* Cv = (const T*)a.C + (size_t)b * L * a.c_stride + (size_t)g * CN;
     const T* dtr = (const T*)a.dt + (size_t)b * L * a.dt_stride + h;
     T* Y = (T*)a.Y + (size_t)b * L * a.y_stride + (size_t)h * P + p0;
-    float* st = a.state + (((size_t)b * H + h) * P + p0) * MF_N;
+    float* st = a.state + (((size_t)b * H + h) * P + p0) * CN;
     const float A_h = -expf(to_f(((const T*)a.A_log)[h]));
     const float dt_b = to_f(((const T*)a.dt_bias)[h]);
     const float D_h = a.has_D ? to_f(((const T*)a.D)[h]) : 0.0f;
 
     const int tid = threadIdx.x;
     const int lane = tid % WAVE;
-    const int w = tid / WAVE;
-    const int l16 = lane % 16, kq = (lane / 16) * 8;
+    const int w = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int li = lane % 16, lq = lane / 16;
+    const int tk = li / 4, tc = li % 4;    // transpose-load row block / column piece
+    const int pw = 16 * w;                 // this wave's columns within the block
 
-    // State tiles owned by wave w: S rows (p) 16*(w%2) .. +16, columns (n)
-    // 64*(w/2) .. +64 = 4 tiles of 16 x 16.
-    const int sp0 = 16 * (w % 2);
-    const int sn0 = 64 * (w / 2);
-    floatx4 sacc[4];
+    // S^T tiles, rounded to T and packed: sp[nt][r] = S[p = pw + li][n = 16 nt + 4 lq + r]
+    s4v sp[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int p = sp0 + (lane / 16) * 4 + r;
-            const int n = sn0 + 16 * j + l16;
-            const float v = rnd<T>(st[(size_t)p * MF_N + n]);
-            sacc[j][r] = v;
-            Sl[p * NPAD + n] = from_f<T>(v);
-        }
+    for (int nt = 0; nt < 8; ++nt)
+        sp[nt] = pack4<T>(*reinterpret_cast<const floatx4*>(st + (size_t)(pw + li) * CN + 16 * nt + 4 * lq));
 
-    for (uint32_t t0 = 0; t0 < L; t0 += MF_Q) {
-        const uint32_t tl = min((uint32_t)MF_Q, L - t0);
-        __syncthreads();
-        // ---- stage B_c, C_c [64 x 128] and X_c^T [32 x 64]; zero past tl ----
+    // D x as one more MFMA: X^T times the diagonal tile D I (exact in T).
+    // Token tile Tt lies in k-slice Tt / 2, where column t = 16 Tt + li has its
+    // diagonal at slot e = 16 (Tt % 2) + li - 8 lq.
+    s8v dfr[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int id = tid + MF_NT * i;          // 1024 chunks of 8 elements
-            const int t = id / 16, c8 = (id % 16) * 8;
-            uint4 bv = make_uint4(0, 0, 0, 0), cv = make_uint4(0, 0, 0, 0);
-            if ((uint32_t)t < tl) {
-                bv = *reinterpret_cast<const uint4*>(Bv + (size_t)(t0 + t) * a.b_stride + c8);
-                cv = *reinterpret_cast<const uint4*>(Cv + (size_t)(t0 + t) * a.c_stride + c8);
+    for (int par = 0; par < 2; ++par)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dfr[par][e] = (e == 16 * par + li - 8 * lq) ? bits_of<T>(D_h) : (short)0;
+
+    // ---- register prefetch of one chunk: uniform chunk base + fixed 32-bit
+    // per-thread byte offsets.  Rows past L (last chunk) re-read row t0:
+    // they only meet M entries that are masked and state weights w = 0. ----
+    const uint32_t brow = tid / 16, bcol = (tid % 16) * 8;
+    const uint32_t xrow = tid / (PB / 8), xcol = (tid % (PB / 8)) * 8;
+    const uint32_t boff = (brow * a.b_stride + bcol) * sizeof(T), coff = (brow * a.c_stride + bcol) * sizeof(T);
+    const uint32_t xoff = (xrow * a.x_stride + xcol) * sizeof(T);
+    u32x4 rb[BV], rc[BV], rx[XV];   // (vector types: a struct uint4 copies
+                                    // through memory and stays in scratch)
+    uint32_t rdt = 0;
+    auto fetch = [&](uint32_t t0) {
+        const uint32_t tl = min((uint32_t)CQ, L - t0);
+        if (tl == CQ) {
+#pragma unroll
+            for (int v = 0; v < BV; ++v) {
+                rb[v] = *reinterpret_cast<const u32x4*>((const char*)(Bv + (size_t)(t0 + BR * v) * a.b_stride) + boff);
+                rc[v] = *reinterpret_cast<const u32x4*>((const char*)(Cv + (size_t)(t0 + BR * v) * a.c_stride) + coff);
             }
-            *reinterpret_cast<uint4*>(Bc + t * NPAD + c8) = bv;
-            *reinterpret_cast<uint4*>(Cc + t * NPAD + c8) = cv;
+#pragma unroll
+            for (int v = 0; v < XV; ++v)
+                rx[v] = *reinterpret_cast<const u32x4*>((const char*)(X + (size_t)(t0 + XR * v) * a.x_stride) + xoff);
+        } else {
+#pragma unroll
+            for (int v = 0; v < BV; ++v) {
+                const uint32_t t = brow + BR * v, tt = t0 + (t < tl ? t : 0);
+                rb[v] = *reinterpret_cast<const u32x4*>(Bv + (size_t)tt * a.b_stride + bcol);
+                rc[v] = *reinterpret_cast<const u32x4*>(Cv + (size_t)tt * a.c_stride + bcol);
+            }
+#pragma unroll
+            for (int v = 0; v < XV; ++v) {
+                const uint32_t t = xrow + XR * v, tt = t0 + (t < tl ? t : 0);
+                rx[v] = *reinterpret_cast<const u32x4*>(X + (size_t)tt * a.x_stride + xcol);
+            }
         }
+        if (w == 0) rdt = raw_of(dtr + (size_t)(t0 + min((uint32_t)lane, tl - 1)) * a.dt_stride);
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int v = 0; v < BV; ++v) {
+            *reinterpret_cast<u32x4*>(Bs + (brow + BR * v) * SPAD + bcol) = rb[v];
+            *reinterpret_cast<u32x4*>(Cs + (brow + BR * v) * SPAD + bcol) = rc[v];
+        }
+#pragma unroll
+        for (int v = 0; v < XV; ++v) *reinterpret_cast<u32x4*>(Xs + (xrow + XR * v) * XP + xcol) = rx[v];
+    };
+    // Wave 0: DT, Lcum, e^{Lcum} and the state weights w of the chunk at t0
+    // into buffer `buf` (tokens past tl get DT = 0, so they drop out).
+    auto scan = [&](uint32_t t0, int buf) {
+        const uint32_t tl = min((uint32_t)CQ, L - t0);
+        float dv = 0.0f;
+        if ((uint32_t)lane < tl) {
+            dv = softplus_f(f_of<T>(rdt) + dt_b);
+            dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
+        }
+        float v = A_h * dv;
+#pragma unroll
+        for (int off = 1; off < WAVE; off <<= 1) {
+            const float o = __shfl_up(v, off, WAVE);
+            if (lane >= off) v += o;
+        }
+        const float l_end = __shfl(v, WAVE - 1, WAVE);
+        LCb[buf][lane] = v;
+        DTb[buf][lane] = dv;
+        ELb[buf][lane] = __expf(v);
+        Wb[buf][lane] = __expf(l_end - v) * dv;
+    };
+
+    const uint32_t nch = (L + CQ - 1) / CQ;
+    fetch(0);
+    stage();
+    if (w == 0) scan(0, 0);
+    if (nch > 1) fetch(CQ);
+    __syncthreads();
+
+    for (uint32_t c = 0; c < nch; ++c) {
+        const uint32_t t0 = c * CQ;
+        const uint32_t tl = min((uint32_t)CQ, L - t0);
+
+        const float* LCs = LCb[c & 1];
+        const float* ELs = ELb[c & 1];
+        const float* Ws = Wb[c & 1];
+
+        // ---- G^T tiles (J <= T) -> M.  Twelve tiles, wave w takes positions
+        // w, w + NW, ...; positions 0 and 4 are the zero upper halves (1,0)
+        // and (3,2) of the k = 32 slices Y reads, which leaves wave 0 time
+        // for the next chunk's dt scan.  (J, T) per position as 2 + 2 bits of
+        // an immediate (an indexed array would be a memory load whose wait
+        // would also wait for the prefetch). ----
         {
-            const int t = tid / 4, c8 = (tid % 4) * 8;   // 256 chunks: 64 tokens x 4
-            uint4 xv = make_uint4(0, 0, 0, 0);
-            if ((uint32_t)t < tl) xv = *reinterpret_cast<const uint4*>(X + (size_t)(t0 + t) * a.x_stride + c8);
-            const T* xe = reinterpret_cast<const T*>(&xv);
+            constexpr int NTL = 12 / NW;
+            constexpr uint64_t JT = 0x1ull | 0x0ull << 4 | 0x4ull << 8 | 0x5ull << 12 | 0xBull << 16 |
+                                    0x8ull << 20 | 0x9ull << 24 | 0xAull << 28 | 0xCull << 32 |
+                                    0xDull << 36 | 0xEull << 40 | 0xFull << 44;
+            const float* DTs = DTb[c & 1];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) Xt[(c8 + e) * QPAD + t] = xe[e];
-        }
-        if (w == 0) {
-            float v = 0.0f, dv = 0.0f;
-            if ((uint32_t)lane < tl) {
-                dv = softplus_f(to_f(dtr[(size_t)(t0 + lane) * a.dt_stride]) + dt_b);
-                dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
-                v = A_h * dv;
-            }
+            for (int i = 0; i < NTL; ++i) {
+                const int kt = w + NW * i;
+                const int jt = (int)(JT >> (4 * kt)) & 15;
+                const int J = jt & 3, Tt = jt >> 2;
+                const int t = 16 * Tt + li;
+                s4v m4 = {0, 0, 0, 0};
+                if (kt != 0 && kt != 4) {
+                    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int off = 1; off < WAVE; off <<= 1) {
-                const float o = __shfl_up(v, off, WAVE);
-                if (lane >= off) v += o;
-            }
-            DT[lane] = dv;
-            Lc[lane] = v;
-        }
-        __syncthreads();
-        const float L_end = Lc[tl - 1];
-
-        // ---- G = C_c . B_c^T, M = r(G o e^{Lc_t - Lc_j} o DT_j) (j <= t) ----
-        {
-            const int t_base = 16 * w;
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                floatx4 gacc = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (jt * 16 <= t_base + 15) {
-#pragma unroll
-                    for (int ks = 0; ks < MF_N / 32; ++ks) {
-                        const frag af = *reinterpret_cast<const frag*>(Cc + (t_base + l16) * NPAD + ks * 32 + kq);
-                        const frag bf = *reinterpret_cast<const frag*>(Bc + (jt * 16 + l16) * NPAD + ks * 32 + kq);
-                        gacc = Op::mma(af, bf, gacc);
+                    for (int ks = 0; ks < CN / 32; ++ks) {
+                        const s8v af = *reinterpret_cast<const s8v*>(Bs + (16 * J + li) * SPAD + 32 * ks + 8 * lq);
+                        const s8v bf = *reinterpret_cast<const s8v*>(Cs + t * SPAD + 32 * ks + 8 * lq);
+                        acc = mma16<T>(af, bf, acc);
                     }
-                }
+                    const float lct = LCs[t];
+                    const floatx4 lcj = *reinterpret_cast<const floatx4*>(LCs + 16 * J + 4 * lq);
+                    const floatx4 dtj = *reinterpret_cast<const floatx4*>(DTs + 16 * J + 4 * lq);
+                    floatx4 m;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = t_base + (lane / 16) * 4 + r;
-                    const int j = jt * 16 + l16;
-                    float m = 0.0f;
-                    if (j <= t && (uint32_t)t < tl) m = gacc[r] * expf(Lc[t] - Lc[j]) * DT[j];
-                    Ml[t * QPAD + j] = from_f<T>(m);
-                }
-            }
-        }
-        __syncthreads();
-
-        // ---- Y tiles: wave w owns rows 16w..16w+15 x the 2 column tiles of PB ----
-        {
-            const int t_base = 16 * w;
-#pragma unroll
-            for (int pt = 0; pt < MF_PB / 16; ++pt) {
-                floatx4 yi = {0.0f, 0.0f, 0.0f, 0.0f}, yo = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int ks = 0; ks < MF_Q / 32; ++ks) {
-                    const frag af = *reinterpret_cast<const frag*>(Ml + (t_base + l16) * QPAD + ks * 32 + kq);
-                    const frag bf = *reinterpret_cast<const frag*>(Xt + (pt * 16 + l16) * QPAD + ks * 32 + kq);
-                    yi = Op::mma(af, bf, yi);
-                }
-#pragma unroll
-                for (int ks = 0; ks < MF_N / 32; ++ks) {
-                    const frag af = *reinterpret_cast<const frag*>(Cc + (t_base + l16) * NPAD + ks * 32 + kq);
-                    const frag bf = *reinterpret_cast<const frag*>(Sl + (pt * 16 + l16) * NPAD + ks * 32 + kq);
-                    yo = Op::mma(af, bf, yo);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = t_base + (lane / 16) * 4 + r;
-                    const int p = pt * 16 + l16;
-                    if ((uint32_t)t < tl) {
-                        const float xc = to_f(Xt[p * QPAD + t]);
-                        const float y = yi[r] + yo[r] * expf(Lc[t]) + D_h * xc;
-                        Y[(size_t)(t0 + t) * a.y_stride + p] = from_f<T>(y);
+                    for (int r = 0; r < 4; ++r) {
+                        const int j = 16 * J + 4 * lq + r;
+                        // Lcum is non-increasing, so the exponent is <= 0 on
+                        // the kept entries; the clamp keeps the others finite
+                        float mv = acc[r] * __expf(fminf(lct - lcj[r], 0.0f)) * dtj[r];
+                        asm volatile("" : "+v"(mv));   // compute, then select (no branch)
+                        m[r] = (j <= t && (uint32_t)t < tl) ? mv : 0.0f;
                     }
+                    m4 = pack4<T>(m);
                 }
+                *reinterpret_cast<s4v*>(Ms + t * MPAD + 16 * J + 4 * lq) = m4;
             }
         }
-        __syncthreads();
+        if (w == 0 && c + 1 < nch) scan(t0 + CQ, (c + 1) & 1);
 
-        // ---- S = r(e^{L_end} S + (X_c o w)^T . B_c), w_j = e^{L_end - Lc_j} DT_j ----
+        // ---- X^T slices of this wave's columns (k = token) ----
+        s8v xf[2];
+#pragma unroll
+        for (int ka = 0; ka < 2; ++ka) {
+            const T* xp = Xs + (32 * ka + 8 * lq + tk) * XP + pw + 4 * tc;
+            xf[ka] = cat8(ld_tr(xp), ld_tr(xp + 4 * XP));
+        }
+
+        // ---- e^{Lcum_t} (S_p . C_t) for the 4 token tiles; S is the
+        // k = n operand as it lies in registers ----
+        floatx4 yacc[4];
+#pragma unroll
+        for (int Tt = 0; Tt < 4; ++Tt) {
+            const int t = 16 * Tt + li;
+            floatx4 yo = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const T* cp = Cs + t * SPAD + 32 * ks + 4 * lq;
+                const s8v cf = cat8(*reinterpret_cast<const s4v*>(cp), *reinterpret_cast<const s4v*>(cp + 16));
+                yo = mma16<T>(cat8(sp[2 * ks], sp[2 * ks + 1]), cf, yo);
+            }
+            const float el = ELs[t];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) yacc[Tt][r] = yo[r] * el;
+        }
+
+        // ---- S^T = r(e^{L_end} S^T + B^T (w o X)) ----
         {
-            const float dch = expf(L_end);
+            const float dch = __expf(LCs[CQ - 1]);
+            s8v wx[2];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int ka = 0; ka < 2; ++ka) {
+                const floatx4 w0 = *reinterpret_cast<const floatx4*>(Ws + 32 * ka + 8 * lq);
+                const floatx4 w1 = *reinterpret_cast<const floatx4*>(Ws + 32 * ka + 8 * lq + 4);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sacc[j][r] *= dch;
-#pragma unroll
-            for (int ks = 0; ks < MF_Q / 32; ++ks) {
-                // A[p][j] = w_j X[j][p], rounded to T (one extra rounding vs the
-                // fp32 sum of the reference)
-                frag af;
-                const int jb = ks * 32 + kq;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int jj = jb + e;
-                    const float wj = ((uint32_t)jj < tl) ? expf(L_end - Lc[jj]) * DT[jj] : 0.0f;
-                    af[e] = from_f<T>(wj * to_f(Xt[(sp0 + l16) * QPAD + jj]));
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    frag bf;
-                    const int n = sn0 + 16 * j + l16;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) bf[e] = Bc[(jb + e) * NPAD + n];
-                    sacc[j] = Op::mma(af, bf, sacc[j]);
+                for (int e = 0; e < 4; ++e) {
+                    wx[ka][e] = bits_of<T>(w0[e] * val_of<T>(xf[ka][e]));
+                    wx[ka][e + 4] = bits_of<T>(w1[e] * val_of<T>(xf[ka][e + 4]));
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int nt = 0; nt < 8; ++nt) {
+                floatx4 acc = unpack4<T>(sp[nt]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float v = rnd<T>(sacc[j][r]);
-                    sacc[j][r] = v;
-                    Sl[(sp0 + (lane / 16) * 4 + r) * NPAD + sn0 + 16 * j + l16] = from_f<T>(v);
+                for (int r = 0; r < 4; ++r) acc[r] *= dch;
+#pragma unroll
+                for (int ka = 0; ka < 2; ++ka) {
+                    const T* bp = Bs + (32 * ka + 8 * lq + tk) * SPAD + 16 * nt + 4 * tc;
+                    const s8v bt = cat8(ld_tr(bp), ld_tr(bp + 4 * SPAD));
+                    acc = mma16<T>(bt, wx[ka], acc);
                 }
+                sp[nt] = pack4<T>(acc);
+            }
         }
+        __syncthreads();   // M complete; staging no longer read
+
+        // Stage the next chunk first: its loads were issued a chunk ago, and
+        // waiting for them before the Y stores below keeps those stores out
+        // of the wait.
+        if (c + 1 < nch) stage();
+
+        // ---- Y^T += X^T M^T + X^T (D I), store ----
+#pragma unroll
+        for (int Tt = 0; Tt < 4; ++Tt) {
+            const int t = 16 * Tt + li;
+#pragma unroll
+            for (int ka = 0; ka < 2; ++ka) {
+                if (ka == 1 && Tt < 2) continue;
+                const s8v mf = *reinterpret_cast<const s8v*>(Ms + t * MPAD + 32 * ka + 8 * lq);
+                yacc[Tt] = mma16<T>(xf[ka], mf, yacc[Tt]);
+            }
+            if (a.has_D) yacc[Tt] = mma16<T>(xf[Tt / 2], dfr[Tt % 2], yacc[Tt]);
+            if ((uint32_t)t < tl)
+                *reinterpret_cast<s4v*>(Y + (size_t)(t0 + t) * a.y_stride + pw + 4 * lq) = pack4<T>(yacc[Tt]);
+        }
+        if (c + 2 < nch) fetch(t0 + 2 * CQ);
+        __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            st[(size_t)(sp0 + (lane / 16) * 4 + r) * MF_N + sn0 + 16 * j + l16] = sacc[j][r];
+    for (int nt = 0; nt < 8; ++nt)
+        *reinterpret_cast<floatx4*>(st + (size_t)(pw + li) * CN + 16 * nt + 4 * lq) = unpack4<T>(sp[nt]);
 }
 
 template <typename T, bool GATE>
@@ -474,15 +581,25 @@ hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a) {
     if (a.batch == 0 || a.H == 0 || a.L == 0) return hipSuccess;
     // A single partial chunk (L < 64, chunk == L) has the same rounding points
     // as chunk 64, so it also takes the MFMA path.
-    const bool chunk_ok = a.chunk == MF_Q || (a.chunk == a.L && a.L < MF_Q);
-    const bool mfma_ok = (a.act != LSSM_F32) && chunk_ok && a.N == MF_N && (a.P % MF_PB) == 0 &&
+    const bool chunk_ok = a.chunk == CQ || (a.chunk == a.L && a.L < CQ);
+    const bool mfma_ok = (a.act != LSSM_F32) && chunk_ok && a.N == CN && (a.P % 32) == 0 &&
                          (a.x_stride % 8 == 0) && (a.b_stride % 8 == 0) && (a.c_stride % 8 == 0) &&
-                         ((uintptr_t)a.X % 16 == 0) && ((uintptr_t)a.B % 16 == 0) &&
-                         ((uintptr_t)a.C % 16 == 0);
+                         (a.y_stride % 4 == 0) && ((uintptr_t)a.X % 16 == 0) &&
+                         ((uintptr_t)a.B % 16 == 0) && ((uintptr_t)a.C % 16 == 0) &&
+                         ((uintptr_t)a.Y % 8 == 0) && ((uintptr_t)a.state % 16 == 0);
     if (mfma_ok) {
-        dim3 grid(a.H * (a.P / MF_PB), a.batch);
-        if (a.act == LSSM_F16) ssd_chunk_mfma_kernel<f16><<<grid, MF_NT, 0, s>>>(a);
-        else ssd_chunk_mfma_kernel<bf16><<<grid, MF_NT, 0, s>>>(a);
+        // Four waves (64 columns of P) per block when that still gives a
+        // block per CU; otherwise two, for more blocks.
+        const bool nw4 = (a.P % 64) == 0 && (size_t)a.batch * a.H * (a.P / 64) >= (size_t)num_cus();
+        if (nw4) {
+            const dim3 grid(a.H * (a.P / 64), a.batch);
+            if (a.act == LSSM_F16) ssd_chunk_mfma_kernel<f16, 4><<<grid, 256, 0, s>>>(a);
+            else ssd_chunk_mfma_kernel<bf16, 4><<<grid, 256, 0, s>>>(a);
+        } else {
+            const dim3 grid(a.H * (a.P / 32), a.batch);
+            if (a.act == LSSM_F16) ssd_chunk_mfma_kernel<f16, 2><<<grid, 128, 0, s>>>(a);
+            else ssd_chunk_mfma_kernel<bf16, 2><<<grid, 128, 0, s>>>(a);
+        }
         return hipGetLastError();
     }
     if (a.chunk > (uint32_t)SC_MAXCK || a.N > (uint32_t)SC_MAXN) return hipErrorInvalidValue;

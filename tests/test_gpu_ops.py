@@ -276,11 +276,15 @@ def test_ssd_chunked_config1_fp32(ctx, rng):
     assert max_rel(host(sd, np.float32), s2) < 1e-3
 
 
+# (4, 130, 64, 1) and P = 128 give at least one block per CU with four waves
+# per block (64 state columns); the others take the two-wave blocks.
 @pytest.mark.parametrize("act", [O.F16, O.BF16])
-@pytest.mark.parametrize("batch,Lq,H,G", [(1, 512, 24, 1), (2, 200, 8, 2), (1, 40, 4, 1), (3, 64, 16, 8)])
-def test_ssd_chunked_mfma_vs_oracle(ctx, rng, act, batch, Lq, H, G):
+@pytest.mark.parametrize("batch,Lq,H,G,P", [(1, 512, 24, 1, 64), (2, 200, 8, 2, 64), (1, 40, 4, 1, 64),
+                                            (3, 64, 16, 8, 64), (4, 130, 64, 1, 64), (2, 100, 6, 2, 32),
+                                            (2, 150, 128, 1, 128)])
+def test_ssd_chunked_mfma_vs_oracle(ctx, rng, act, batch, Lq, H, G, P):
     L = _lib()
-    P, N = 64, 128
+    N = 128
     X, B, Cc, dt, dtb, A_log, D = _ssd_inputs(rng, batch, Lq, H, P, N, G, act)
     st = (rng.standard_normal((batch, H, P, N)) * 0.2).astype(np.float32)
     ck = min(64, Lq)
