@@ -215,6 +215,301 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile GEMM.  512 threads own a 256 x 128 tile of Y.  Waves 0..3
+// compute: each owns 128 x 64 = 4 x 2 v_mfma_f32_32x32x16, reads its LDS
+// fragments one k16 sub-step ahead, and between the MFMAs issues the
+// global -> LDS DMA (global_load_lds_dwordx4: lane i of a wave writes bytes
+// 16 i .. 16 i + 15 of a 1 KiB run, i.e. 8 tile rows) of X two K steps ahead
+// into a 3-stage ring.  Waves 4..7 handle W: quantized W is loaded into
+// registers and dequantized (to r(q s) in the activation type, as the
+// reference GEMM does) into a 2-stage ring one step ahead; dense W goes by
+// DMA into a 3-stage ring.  So loads and dequantization run beside the
+// MFMAs instead of between them.  One barrier per K step.  LDS rows are 64
+// elements (128 B) whose 16-byte slots are XOR-swizzled by row % 8, so the
+// fragment reads of 8 consecutive rows hit distinct banks without padding.
+// ---------------------------------------------------------------------------
+constexpr int G2M = 256, G2N = 128, G2K = 64, G2T = 512;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 16 consecutive quantized weights of one row: raw bits + fp16 scale bits.
+template <int FMT> struct WRaw { u32x2 q; uint32_t s; };
+template <> struct WRaw<LSSM_W_Q8_G32> { u32x4 q; uint32_t s; };
+
+template <typename T> __device__ __forceinline__ uint32_t pk2(float lo, float hi) {
+    if constexpr (__is_same(T, bf16)) {
+        typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, v2{(__bf16)lo, (__bf16)hi});
+    } else {
+        typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, v2{(_Float16)lo, (_Float16)hi});
+    }
+}
+
+// r(q s) for 16 weights -> 8 packed pairs.  int4: the unsigned nibble
+// u = q + 8 is placed by v_perm into the mantissa of the fp32 128 + u, and
+// fma(128 + u, s, -136 s) = q s exactly (-136 s is exact: 8 + 11 bits); int8:
+// u = q + 128 as a float and fma(u, s, -128 s).  One rounding, at the pack.
+template <int FMT, typename T>
+__device__ __forceinline__ void dequant16(const WRaw<FMT>& r, uint32_t out[8]) {
+    const float s = fp16_bits_to_f((uint16_t)r.s);
+    if constexpr (FMT == LSSM_W_Q8_G32) {
+        const float c = -128.0f * s;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d = r.q[i] ^ 0x80808080u;
+            // (byte -> float converts to v_cvt_f32_ubyte{0..3})
+            const float f0 = (float)(d & 0xFFu), f1 = (float)((d >> 8) & 0xFFu);
+            const float f2 = (float)((d >> 16) & 0xFFu), f3 = (float)(d >> 24);
+            out[2 * i] = pk2<T>(__builtin_fmaf(f0, s, c), __builtin_fmaf(f1, s, c));
+            out[2 * i + 1] = pk2<T>(__builtin_fmaf(f2, s, c), __builtin_fmaf(f3, s, c));
+        }
+    } else {
+        const float c = -136.0f * s;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t d = r.q[i] ^ 0x88888888u;
+            const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+            // element 2b is byte b of lo, element 2b + 1 byte b of hi
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t sel = 0x04000C0Cu | ((uint32_t)b << 16);
+                const float e0 = __uint_as_float(__builtin_amdgcn_perm(0x43434343u, lo, sel));
+                const float e1 = __uint_as_float(__builtin_amdgcn_perm(0x43434343u, hi, sel));
+                out[4 * i + b] = pk2<T>(__builtin_fmaf(e0, s, c), __builtin_fmaf(e1, s, c));
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void lds_dma16(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+// The same DMA as inline asm, for waves that also read LDS: the compiler does
+// not see it, so it does not wait for it before every LDS read (it cannot
+// tell which LDS bytes a DMA writes); the issuing wave waits with an explicit
+// vmcnt.  m0 (the LDS base of the 1 KiB run) is saved and restored.
+__device__ __forceinline__ void lds_dma16_asm(const void* g, uint32_t lds_byte) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(lds_byte)
+        : "memory");
+}
+template <typename T> __device__ __forceinline__ uint32_t lds_addr(const T* p) {
+    return (uint32_t)(size_t)((const __attribute__((address_space(3))) T*)p);
+}
+
+template <int FMT, typename T, int EPI>
+__global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
+    constexpr bool DENSE = FMT == LSSM_W_DENSE;
+    constexpr int SB = DENSE ? 3 : 2;             // W stages (dense W also goes by DMA)
+    __shared__ __attribute__((aligned(16))) T As[3][G2M * G2K];
+    __shared__ __attribute__((aligned(16))) T Bs[SB][G2N * G2K];
+    using Op = MfmaOp<T>;
+    using frag = typename Op::frag;
+
+    const int t = threadIdx.x;
+    const int lane = t % WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(t / WAVE);
+    const uint32_t m0 = blockIdx.y * G2M, n0 = blockIdx.x * G2N;
+    const uint32_t K = a.K, KT = K / G2K;
+    // a barrier without __syncthreads' release fence (which would wait for
+    // every DMA in flight); the empty asm keeps memory operations in place
+    auto barrier = [] {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    if (w >= 4) {
+        // ---------------- producers: waves 4..7, W only ----------------
+        const int q = w - 4;
+        const uint32_t p = t - 256;
+        if constexpr (DENSE) {
+            // by DMA: producer wave q fills tile rows 32 q .. + 32, 8 rows per
+            // instruction (lane i: row + i / 8, physical slot i % 8 = logical
+            // slot (i % 8) ^ (i / 8)); rows past N re-read row N - 1.
+            const uint32_t sl = (lane % 8) ^ (lane / 8);
+            const char* wq[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t n = min(n0 + 32 * q + 8 * j + lane / 8, a.N - 1);
+                wq[j] = (const char*)a.w + ((size_t)n * K + 8 * sl) * sizeof(T);
+            }
+            auto dma_w = [&](uint32_t kt) {
+                T* dst = Bs[kt % SB] + (32 * q) * G2K;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) lds_dma16(wq[j] + (size_t)kt * G2K * sizeof(T), dst + 8 * j * G2K);
+            };
+            // 4 DMAs per step: vmcnt(4) = the previous step's are done
+            dma_w(0);
+            dma_w(min(1u, KT - 1));
+            __builtin_amdgcn_s_waitcnt(0x0F74);
+            barrier();
+            for (uint32_t kt = 0; kt < KT; ++kt) {
+                dma_w(min(kt + 2, KT - 1));
+                __builtin_amdgcn_s_waitcnt(0x0F74);
+                barrier();
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            return;
+        } else {
+            // thread p owns row p / 2 of the tile, weights (p % 2) * 32 .. + 32
+            // of a step; step k + 2's are loaded into registers at the start
+            // of step k (two register sets) and dequantized into LDS in step
+            // k + 1.
+            const uint32_t br = p / 2, bh = p % 2;
+            constexpr uint32_t GS = FMT == LSSM_W_Q4_G64 ? 64 : 32;
+            const uint32_t nrow = min(n0 + br, a.N - 1);
+            const char* wq = (const char*)a.w + (size_t)nrow * (FMT == LSSM_W_Q8_G32 ? K : K / 2);
+            const uint16_t* sp = (const uint16_t*)a.s + (size_t)nrow * (K / GS);
+            using R = WRaw<FMT>;
+            auto load_w = [&](uint32_t kt, R (&r)[2]) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t k = kt * G2K + 32 * bh + 16 * h;
+                    if constexpr (FMT == LSSM_W_Q8_G32) r[h].q = *reinterpret_cast<const u32x4*>(wq + k);
+                    else r[h].q = *reinterpret_cast<const u32x2*>(wq + k / 2);
+                    r[h].s = sp[k / GS];
+                }
+            };
+            auto store_w = [&](uint32_t kt, const R (&r)[2]) {
+                T* Brow = Bs[kt % SB] + br * G2K;
+                const uint32_t sw = br % 8;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t d[8];
+                    dequant16<FMT, T>(r[h], d);
+                    const uint32_t s0 = 4 * bh + 2 * h;
+                    *reinterpret_cast<u32x4*>(Brow + 8 * (s0 ^ sw)) = u32x4{d[0], d[1], d[2], d[3]};
+                    *reinterpret_cast<u32x4*>(Brow + 8 * ((s0 + 1) ^ sw)) = u32x4{d[4], d[5], d[6], d[7]};
+                }
+            };
+            R r0[2], r1[2];
+            load_w(0, r0);
+            load_w(min(1u, KT - 1), r1);
+            store_w(0, r0);
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            barrier();
+            // step kt: load step kt + 2, then write step kt + 1 (its loads were
+            // issued a step ago).  Branch-free: past the end it re-loads step
+            // KT - 1 and writes the idle stage.
+            auto step = [&](uint32_t kt, R (&ld)[2], const R (&wr)[2]) {
+                load_w(min(kt + 2, KT - 1), ld);
+                __builtin_amdgcn_sched_barrier(0);    // loads first
+                store_w(kt + 1, wr);
+                __builtin_amdgcn_s_waitcnt(0xC07F);
+                barrier();
+            };
+            uint32_t kt = 0;
+            for (; kt + 1 < KT; kt += 2) {
+                step(kt, r0, r1);
+                step(kt + 1, r1, r0);
+            }
+            if (kt < KT) step(kt, r0, r1);
+            return;
+        }
+    }
+
+    // ---------------- consumers: waves 0..3, 128 x 64 of Y each ----------------
+    // They also DMA X: wave c fills tile rows 64 c .. + 64 of the stage two
+    // steps ahead, 8 rows per instruction (lane i: row + i / 8, physical slot
+    // i % 8 = logical slot (i % 8) ^ (i / 8)); rows past M re-read row M - 1.
+    const int wm = w / 2, wn = w % 2;
+    const uint32_t xl = (lane % 8) ^ (lane / 8);
+    uint32_t xo[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t m = min(m0 + 64 * w + 8 * j + lane / 8, a.M - 1);
+        xo[j] = (m * a.x_stride + 8 * xl) * (uint32_t)sizeof(T);
+    }
+    const uint32_t as0 = lds_addr(&As[0][0]) + (64 * w) * G2K * (uint32_t)sizeof(T);
+    auto dma_x = [&](uint32_t kt, int j0, int j1) {
+        const char* base = (const char*)a.x + (size_t)kt * G2K * sizeof(T);
+        const uint32_t dst = as0 + (kt % 3) * (G2M * G2K * (uint32_t)sizeof(T));
+        for (int j = j0; j < j1; ++j) lds_dma16_asm(base + xo[j], dst + 8 * j * G2K * (uint32_t)sizeof(T));
+    };
+
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    // fragment offsets (elements): row & 7 == lane & 7 for every fragment
+    uint32_t fo[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) fo[ks] = (lane % 32) * G2K + 8 * ((2 * ks + lane / 32) ^ (lane % 8));
+
+    // 8 DMAs per step: vmcnt(8) = the previous step's are done
+    dma_x(0, 0, 8);
+    dma_x(min(1u, KT - 1), 0, 8);
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    barrier();                                    // step 0 in LDS
+    for (uint32_t kt = 0; kt < KT; ++kt) {
+        const T* Ab = As[kt % 3] + (wm * 128) * G2K;
+        const T* Bb = Bs[kt % SB] + (wn * 64) * G2K;
+        const uint32_t k2 = min(kt + 2, KT - 1);
+        frag af[2][4], bfr[2][2];
+        auto rd = [&](int ks, frag (&fa)[4], frag (&fb)[2]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const frag*>(Ab + 32 * i * G2K + fo[ks]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const frag*>(Bb + 32 * j * G2K + fo[ks]);
+        };
+        rd(0, af[0], bfr[0]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks + 1 < 4) rd(ks + 1, af[(ks + 1) % 2], bfr[(ks + 1) % 2]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(af[ks % 2][i], bfr[ks % 2][j], acc[i][j]);
+            // next sub-step's fragment reads ahead of this sub-step's MFMAs
+            // (the asm DMA below ends the scheduling region)
+            if (ks == 0) __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+            else if (ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            dma_x(k2, 2 * ks, 2 * ks + 2);        // step kt + 2's X, 2 runs per sub-step
+        }
+        // step kt + 1's X in LDS, this step's fragment reads done
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+        barrier();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // D layout of v_mfma_f32_32x32x*: element r of lane l is
+    // row (r/4)*8 + (l/32)*4 + r%4, column l%32.
+    T* Y = (T*)a.y;
+    const T* Rz = (const T*)a.res;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t n = n0 + wn * 64 + j * 32 + lane % 32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = m0 + wm * 128 + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + r % 4;
+                if (m < a.M && n < a.N) {
+                    const size_t yi = (size_t)m * a.y_stride + n;
+                    float v = acc[i][j][r];
+                    if (EPI == LSSM_EPI_SILU) v = silu_f(v);
+                    if (EPI == LSSM_EPI_ADD) v = to_f(Rz[yi]) + rnd<T>(v);
+                    Y[yi] = from_f<T>(v);
+                }
+            }
+        }
+    }
+}
+
 // Plain per-output kernel for fp32 activations and unaligned shapes: one
 // thread per output; the dequantized weight is rounded to the activation dtype
 // when round_dequant != 0 (GEMM semantics) and exact otherwise (GEMV).
@@ -256,6 +551,17 @@ __global__ void gemm_simple_kernel(GemmArgs a) {
 
 template <int FMT, typename T>
 hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
+    // the large tile for prefill-sized M; X byte offsets within a 256-row
+    // tile fit 32 bits
+    if (a.M > 128 && (uint64_t)a.M * a.x_stride * sizeof(T) < (1ull << 31)) {
+        dim3 grid((a.N + G2N - 1) / G2N, (a.M + G2M - 1) / G2M);
+        switch (a.epi) {
+            case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU><<<grid, G2T, 0, s>>>(a); break;
+            case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD><<<grid, G2T, 0, s>>>(a); break;
+            default: gemm2_kernel<FMT, T, LSSM_EPI_NONE><<<grid, G2T, 0, s>>>(a); break;
+        }
+        return hipGetLastError();
+    }
     dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
     switch (a.epi) {
         case LSSM_EPI_SILU: gemm_kernel<FMT, T, LSSM_EPI_SILU><<<grid, NT, 0, s>>>(a); break;

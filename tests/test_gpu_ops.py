@@ -71,6 +71,20 @@ def test_gemm_vs_oracle(ctx, rng, act, wfmt, M):
     assert_close(act_host(y, act), ref, act, bound, "gemm")
 
 
+@pytest.mark.parametrize("wfmt", [O.W_Q4_G64, O.W_Q8_G32, O.W_DENSE])
+@pytest.mark.parametrize("K", [64, 192])
+def test_gemm_one_and_odd_k_steps(ctx, rng, wfmt, K):
+    """Large-tile GEMM with 1 and 3 K steps of 64 (the pipeline's tail paths),
+    M and N one past a tile edge."""
+    act, M, N = O.BF16, 257, 129
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    y = empty((M, N), act)
+    ctx.linear(dev(x), dev(w), None if s is None else dev(s), y, M, N, K, wfmt, act)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, round_dequant=1)
+    assert_close(act_host(y, act), ref, act, 1.6e-2, "gemm")
+
+
 @pytest.mark.parametrize("act", [O.F16, O.BF16, O.F32])
 @pytest.mark.parametrize("M", [2, 130])
 def test_linear_epilogues(ctx, rng, act, M):
