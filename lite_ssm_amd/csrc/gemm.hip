@@ -510,6 +510,133 @@ __global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM for decode batches (5 <= M <= 64): the weights are streamed once.
+// A block covers 16 rows of W; its KS waves split K into slices of UPW units,
+// and the slices are summed in LDS.  A lane loads 16 bytes of one W row per
+// unit (int4: 32 k, int8: 16, dense: 8) and dequantizes them (to r(q s), GEMM
+// semantics) straight into v_mfma_f32_16x16x32 A operands: MFMA k-step s of a
+// unit takes, in lane group q = lane / 16, the k = unit + KPL q + 8 s .. + 8
+// (the k order inside an MFMA is free as long as both operands follow it), so
+// x is read as matching 16-byte runs of its rows (L2-resident, shared by all
+// blocks).  All loads of a wave are issued before its first MFMA.
+// ---------------------------------------------------------------------------
+template <int FMT> struct SkUnit {
+    static constexpr int KPL = FMT == LSSM_W_DENSE ? 8 : (FMT == LSSM_W_Q8_G32 ? 16 : 32);
+    static constexpr int U = 4 * KPL;            // k per unit
+    static constexpr int STEPS = KPL / 8;        // MFMA k-steps per unit
+};
+constexpr int SK_MAXW = 16;                      // K slices (waves) per block
+
+template <typename T> __device__ __forceinline__ floatx4 mma16x32(u32x4 a, u32x4 b, floatx4 c) {
+    if constexpr (__is_same(T, bf16))
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+
+template <int FMT, typename T, int EPI, int MT, int UPW>
+__global__ __launch_bounds__(64 * SK_MAXW) void gemm_skinny_kernel(GemmArgs a) {
+    using SU = SkUnit<FMT>;
+    constexpr int KPL = SU::KPL, U = SU::U, STEPS = SU::STEPS;
+    constexpr uint32_t GS = FMT == LSSM_W_Q4_G64 ? 64 : 32;
+    __shared__ floatx4 red[SK_MAXW - 1][MT][64];
+
+    const int lane = threadIdx.x % WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    const int KS = blockDim.x / WAVE;
+    const int li = lane % 16, lq = lane / 16;
+    const uint32_t n0 = blockIdx.x * 16;
+    const uint32_t K = a.K, kb = w * (UPW * U);
+    const uint32_t n = min(n0 + li, a.N - 1);
+
+    const char* wrow;
+    const uint16_t* srow = nullptr;
+    if constexpr (FMT == LSSM_W_DENSE) wrow = (const char*)a.w + (size_t)n * K * sizeof(T);
+    else {
+        wrow = (const char*)a.w + (size_t)n * (FMT == LSSM_W_Q8_G32 ? K : K / 2);
+        srow = (const uint16_t*)a.s + (size_t)n * (K / GS);
+    }
+    const T* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = (const T*)a.x + (size_t)min(16u * mt + li, a.M - 1) * a.x_stride;
+
+    struct Unit { u32x4 w; uint32_t s; u32x4 x[MT][STEPS]; };
+    Unit r[UPW];
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu) {
+        const uint32_t k = kb + uu * U + KPL * lq;
+        if constexpr (FMT == LSSM_W_DENSE) r[uu].w = *reinterpret_cast<const u32x4*>(wrow + (size_t)k * sizeof(T));
+        else if constexpr (FMT == LSSM_W_Q8_G32) r[uu].w = *reinterpret_cast<const u32x4*>(wrow + k);
+        else r[uu].w = *reinterpret_cast<const u32x4*>(wrow + k / 2);
+        if constexpr (FMT != LSSM_W_DENSE) r[uu].s = srow[k / GS];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int st = 0; st < STEPS; ++st) r[uu].x[mt][st] = *reinterpret_cast<const u32x4*>(xrow[mt] + k + 8 * st);
+    }
+    // all loads in flight before the first MFMA (when they fit the registers:
+    // 16-wave blocks leave 128 VGPRs)
+    if constexpr (UPW * MT <= 4) __builtin_amdgcn_sched_barrier(0);
+    floatx4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu) {
+        u32x4 af[STEPS];
+        if constexpr (FMT == LSSM_W_DENSE) {
+            af[0] = r[uu].w;
+        } else if constexpr (FMT == LSSM_W_Q8_G32) {
+            WRaw<FMT> q{r[uu].w, r[uu].s};
+            uint32_t d[8];
+            dequant16<FMT, T>(q, d);
+            af[0] = u32x4{d[0], d[1], d[2], d[3]};
+            af[1] = u32x4{d[4], d[5], d[6], d[7]};
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                WRaw<FMT> q{u32x2{r[uu].w[2 * h], r[uu].w[2 * h + 1]}, r[uu].s};
+                uint32_t d[8];
+                dequant16<FMT, T>(q, d);
+                af[2 * h] = u32x4{d[0], d[1], d[2], d[3]};
+                af[2 * h + 1] = u32x4{d[4], d[5], d[6], d[7]};
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = mma16x32<T>(af[st], r[uu].x[mt][st], acc[mt]);
+    }
+
+    // sum the K slices; wave 0 stores.  D element r of lane l: row
+    // 4 (l / 16) + r (W row n0 + .), column l % 16 (x row 16 mt + .).
+    if (w > 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[w - 1][mt][lane] = acc[mt];
+    }
+    __syncthreads();
+    if (w != 0) return;
+    T* Y = (T*)a.y;
+    const T* R = (const T*)a.res;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        floatx4 v = acc[mt];
+        for (int q = 0; q < KS - 1; ++q) v += red[q][mt][lane];
+        const uint32_t m = 16 * mt + li;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t nn = n0 + 4 * lq + rr;
+            if (nn >= a.N) continue;
+            const size_t yi = (size_t)m * a.y_stride + nn;
+            float o = v[rr];
+            if (EPI == LSSM_EPI_SILU) o = silu_f(o);
+            if (EPI == LSSM_EPI_ADD) o = to_f(R[yi]) + rnd<T>(o);
+            Y[yi] = from_f<T>(o);
+        }
+    }
+}
+
 // Plain per-output kernel for fp32 activations and unaligned shapes: one
 // thread per output; the dequantized weight is rounded to the activation dtype
 // when round_dequant != 0 (GEMM semantics) and exact otherwise (GEMV).
@@ -549,8 +676,48 @@ __global__ void gemm_simple_kernel(GemmArgs a) {
     ((T*)a.y)[yi] = from_f<T>(v);
 }
 
+template <int FMT, typename T, int MT, int UPW>
+hipError_t go_skinny(hipStream_t s, const GemmArgs& a) {
+    const dim3 grid((a.N + 15) / 16);
+    const dim3 block(64 * (a.K / (UPW * SkUnit<FMT>::U)));
+    switch (a.epi) {
+        case LSSM_EPI_SILU: gemm_skinny_kernel<FMT, T, LSSM_EPI_SILU, MT, UPW><<<grid, block, 0, s>>>(a); break;
+        case LSSM_EPI_ADD: gemm_skinny_kernel<FMT, T, LSSM_EPI_ADD, MT, UPW><<<grid, block, 0, s>>>(a); break;
+        default: gemm_skinny_kernel<FMT, T, LSSM_EPI_NONE, MT, UPW><<<grid, block, 0, s>>>(a); break;
+    }
+    return hipGetLastError();
+}
+
+// Units per wave for the skinny GEMM: preferably 4 / MT (all of a wave's loads
+// then fit in registers at once), else the nearest that splits K into at most
+// SK_MAXW whole slices; 0 = not supported.
+template <int FMT> int skinny_upw(uint32_t K, int mt) {
+    constexpr uint32_t U = SkUnit<FMT>::U;
+    const int pref = 4 / mt;
+    const int order[3][3] = {{1, 2, 4}, {2, 1, 4}, {4, 2, 1}};
+    for (int upw : order[pref == 1 ? 0 : (pref == 2 ? 1 : 2)])
+        if (K % (upw * U) == 0 && K / (upw * U) <= (uint32_t)SK_MAXW) return upw;
+    return 0;
+}
+
+template <int FMT, typename T, int MT>
+hipError_t go_skinny_mt(hipStream_t s, const GemmArgs& a, int upw) {
+    if (upw == 4) return go_skinny<FMT, T, MT, 4>(s, a);
+    if (upw == 2) return go_skinny<FMT, T, MT, 2>(s, a);
+    return go_skinny<FMT, T, MT, 1>(s, a);
+}
+
 template <int FMT, typename T>
 hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
+    // decode batches: weights streamed once
+    if (a.M <= 64) {
+        const int mt = a.M <= 16 ? 1 : (a.M <= 32 ? 2 : 4);
+        if (const int upw = skinny_upw<FMT>(a.K, mt)) {
+            if (mt == 1) return go_skinny_mt<FMT, T, 1>(s, a, upw);
+            if (mt == 2) return go_skinny_mt<FMT, T, 2>(s, a, upw);
+            return go_skinny_mt<FMT, T, 4>(s, a, upw);
+        }
+    }
     // the large tile for prefill-sized M; X byte offsets within a 256-row
     // tile fit 32 bits
     if (a.M > 128 && (uint64_t)a.M * a.x_stride * sizeof(T) < (1ull << 31)) {

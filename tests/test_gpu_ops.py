@@ -71,6 +71,38 @@ def test_gemm_vs_oracle(ctx, rng, act, wfmt, M):
     assert_close(act_host(y, act), ref, act, bound, "gemm")
 
 
+@pytest.mark.parametrize("act", [O.F16, O.BF16])
+@pytest.mark.parametrize("wfmt", ALL_FMTS)
+@pytest.mark.parametrize("M", [7, 16, 40, 64])
+def test_gemm_decode_batch_vs_oracle(ctx, rng, act, wfmt, M):
+    """Decode batches (5 <= M <= 64): the weight-streaming GEMM, N not a
+    multiple of its 16-row tile."""
+    N, K = 300, 1024
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    y = empty((M, N), act)
+    ctx.linear(dev(x), dev(w), None if s is None else dev(s), y, M, N, K, wfmt, act)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, round_dequant=1)
+    assert_close(act_host(y, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2}[act], "gemm")
+
+
+@pytest.mark.parametrize("act", [O.F16, O.BF16])
+def test_gemm_decode_batch_epilogues(ctx, rng, act):
+    L = _lib()
+    M, N, K, wfmt = 16, 256, 512, O.W_Q4_G64
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    res = O.to_act(rng.standard_normal((M, N)), act)
+    yd = dev(res)
+    ctx.linear(dev(x), dev(w), dev(s), yd, M, N, K, wfmt, act, epi=L.EPI_ADD, residual=yd)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, epi=O.EPI_ADD, residual=res, round_dequant=1)
+    assert_close(act_host(yd, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2}[act], "add")
+    ys = empty((M, N), act)
+    ctx.linear(dev(x), dev(w), dev(s), ys, M, N, K, wfmt, act, epi=L.EPI_SILU)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, epi=O.EPI_SILU, round_dequant=1)
+    assert_close(act_host(ys, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2}[act], "silu")
+
+
 @pytest.mark.parametrize("wfmt", [O.W_Q4_G64, O.W_Q8_G32, O.W_DENSE])
 @pytest.mark.parametrize("K", [64, 192])
 def test_gemm_one_and_odd_k_steps(ctx, rng, wfmt, K):
