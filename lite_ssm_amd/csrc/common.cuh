@@ -42,6 +42,11 @@ __device__ __forceinline__ float silu_fast(float v) {
 }
 __device__ __forceinline__ float softplus_f(float v) { return (v > 20.0f) ? v : logf(1.0f + expf(v)); }
 
+// Value of the 16-bit pattern b of a T (fp16 or bf16).
+template <typename T> __device__ __forceinline__ float f_of_bits(uint16_t b) {
+    return to_f(__builtin_bit_cast(T, b));
+}
+
 __device__ __forceinline__ float fp16_bits_to_f(uint16_t b) {
     union { uint16_t u; f16 h; } c;
     c.u = b;

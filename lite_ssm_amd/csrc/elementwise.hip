@@ -4,6 +4,8 @@
 // Arithmetic follows shaders/norm.metal:52-79, activations.metal:12-87 and
 // conv1d.metal:35-137; storage is fp16 / bf16 / fp32, math fp32.
 #include <cfloat>
+#include <initializer_list>
+#include <utility>
 
 #include "common.cuh"
 #include "internal.hpp"
@@ -23,6 +25,22 @@ namespace lssm {
             __VA_ARGS__;                                 \
         }                                                \
     } while (0)
+
+// 8 fp16 / bf16 values in a 16-byte vector register.
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+template <typename T> __device__ __forceinline__ float el8(v4u v, int e) {
+    const uint32_t d = v[e / 2];
+    return f_of_bits<T>((uint16_t)((e & 1) ? (d >> 16) : (d & 0xFFFF)));
+}
+template <typename T> __device__ __forceinline__ uint32_t bits_t(float f) {
+    return __builtin_bit_cast(uint16_t, from_f<T>(f));
+}
+template <typename T> __device__ __forceinline__ v4u pack8(const float (&f)[8]) {
+    v4u r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = bits_t<T>(f[2 * i]) | (bits_t<T>(f[2 * i + 1]) << 16);
+    return r;
+}
 
 constexpr int NT = 256;
 
@@ -66,6 +84,91 @@ __global__ __launch_bounds__(NT) void gated_rmsnorm_kernel(const T* __restrict__
     for (uint32_t i = threadIdx.x; i < dim; i += NT) {
         float g = rnd<T>(silu_f(to_f(zr[i])) * to_f(yr[i]));
         o[i] = from_f<T>(g * to_f(w[i]) * rrms);
+    }
+}
+
+// Vectorized norms: one wave per row, 8 elements (16 bytes) per lane per
+// chunk, the row held in registers between the sum of squares and the
+// scaled store, so every input is read once.  NCH = chunks of 512 elements
+// per row (dim <= 512 NCH).  Same arithmetic as the kernels above; the SiLU
+// of the gate uses the hardware exp / reciprocal (the reference builds its
+// kernels with fast math).
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(const T* __restrict__ x, uint32_t xs,
+                                                          const T* __restrict__ w, T* __restrict__ y,
+                                                          uint32_t ys, uint32_t rows, uint32_t dim,
+                                                          float eps) {
+    const uint32_t row = blockIdx.x * 4 + threadIdx.x / WAVE;
+    if (row >= rows) return;
+    const uint32_t lane = threadIdx.x % WAVE;
+    const T* xr = x + (size_t)row * xs;
+    v4u xv[NCH];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = (c * WAVE + lane) * 8;
+        xv[c] = i < dim ? *reinterpret_cast<const v4u*>(xr + i) : v4u{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = el8<T>(xv[c], e);
+            ss += v * v;
+        }
+    }
+    ss = wave_sum(ss);
+    const float rrms = 1.0f / sqrtf(ss / (float)dim + eps);
+    T* yr = y + (size_t)row * ys;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = (c * WAVE + lane) * 8;
+        if (i >= dim) break;
+        const v4u wv = *reinterpret_cast<const v4u*>(w + i);
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = el8<T>(xv[c], e) * el8<T>(wv, e) * rrms;
+        *reinterpret_cast<v4u*>(yr + i) = pack8<T>(o);
+    }
+}
+
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void gated_rmsnorm_wave_kernel(
+    const T* __restrict__ z, uint32_t zs, const T* __restrict__ yv, uint32_t yst,
+    const T* __restrict__ w, T* __restrict__ out, uint32_t rows, uint32_t dim, float eps) {
+    const uint32_t row = blockIdx.x * 4 + threadIdx.x / WAVE;
+    if (row >= rows) return;
+    const uint32_t lane = threadIdx.x % WAVE;
+    const T* zr = z + (size_t)row * zs;
+    const T* yr = yv + (size_t)row * yst;
+    v4u zv[NCH], yy[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = (c * WAVE + lane) * 8;
+        zv[c] = i < dim ? *reinterpret_cast<const v4u*>(zr + i) : v4u{0, 0, 0, 0};
+        yy[c] = i < dim ? *reinterpret_cast<const v4u*>(yr + i) : v4u{0, 0, 0, 0};
+    }
+    v4u gv[NCH];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        float g[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            g[e] = rnd<T>(silu_fast(el8<T>(zv[c], e)) * el8<T>(yy[c], e));
+            ss += g[e] * g[e];
+        }
+        gv[c] = pack8<T>(g);
+    }
+    ss = wave_sum(ss);
+    const float rrms = 1.0f / sqrtf(ss / (float)dim + eps);
+    T* o = out + (size_t)row * dim;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const uint32_t i = (c * WAVE + lane) * 8;
+        if (i >= dim) break;
+        const v4u wv = *reinterpret_cast<const v4u*>(w + i);
+        float r[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = el8<T>(gv[c], e) * el8<T>(wv, e) * rrms;
+        *reinterpret_cast<v4u*>(o + i) = pack8<T>(r);
     }
 }
 
@@ -146,51 +249,42 @@ __global__ __launch_bounds__(256) void conv1d_vec_kernel(const T* __restrict__ x
     const uint32_t t0 = blockIdx.y * CONV_CT;
     const uint32_t b = blockIdx.z;
     const T* xb = x + (size_t)b * L * xs + d0;
-    uint4 win[CONV_CT + 3];
+    // the window as vector registers; elements are taken out by shifts (an
+    // element address would put the array in scratch memory)
+    v4u win[CONV_CT + 3];
 #pragma unroll
     for (int i = 0; i < CONV_CT + 3; ++i) {
         const int t = (int)t0 + i - 3;
-        win[i] = (t >= 0 && t < (int)L) ? *reinterpret_cast<const uint4*>(xb + (size_t)t * xs)
-                                        : make_uint4(0, 0, 0, 0);
+        win[i] = (t >= 0 && t < (int)L) ? *reinterpret_cast<const v4u*>(xb + (size_t)t * xs)
+                                        : v4u{0, 0, 0, 0};
     }
     // taps w[d][0..3] of the 8 channels: 64 contiguous bytes
     float wf[8][4], bf[8];
     {
-        const uint4* w4 = reinterpret_cast<const uint4*>(w + (size_t)d0 * 4);
+        const v4u* w4 = reinterpret_cast<const v4u*>(w + (size_t)d0 * 4);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint4 v = w4[q];
-            const T* tv = reinterpret_cast<const T*>(&v);
+            const v4u v = w4[q];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) wf[2 * q + e / 4][e % 4] = to_f(tv[e]);
+            for (int e = 0; e < 8; ++e) wf[2 * q + e / 4][e % 4] = el8<T>(v, e);
         }
-        if (bias) {
-            const uint4 v = *reinterpret_cast<const uint4*>(bias + d0);
-            const T* tv = reinterpret_cast<const T*>(&v);
+        const v4u bv = bias ? *reinterpret_cast<const v4u*>(bias + d0) : v4u{0, 0, 0, 0};
 #pragma unroll
-            for (int c = 0; c < 8; ++c) bf[c] = to_f(tv[c]);
-        } else {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) bf[c] = 0.0f;
-        }
+        for (int c = 0; c < 8; ++c) bf[c] = el8<T>(bv, c);
     }
     T* yb = y + ((size_t)b * L + t0) * ys + d0;
 #pragma unroll
     for (int i = 0; i < CONV_CT; ++i) {
-        if (t0 + i >= L) break;
-        uint4 out;
-        T* ov = reinterpret_cast<T*>(&out);
+        float o[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             float acc = bf[c];
 #pragma unroll
-            for (int tap = 0; tap < 4; ++tap)
-                acc += wf[c][tap] * to_f(reinterpret_cast<const T*>(&win[i + tap])[c]);
-            float o = rnd<T>(acc);
-            if (SILU) o = silu_f(o);
-            ov[c] = from_f<T>(o);
+            for (int tap = 0; tap < 4; ++tap) acc += wf[c][tap] * el8<T>(win[i + tap], c);
+            o[c] = rnd<T>(acc);
+            if (SILU) o[c] = silu_fast(o[c]);
         }
-        *reinterpret_cast<uint4*>(yb + (size_t)i * ys) = out;
+        if (t0 + i < L) *reinterpret_cast<v4u*>(yb + (size_t)i * ys) = pack8<T>(o);
     }
   }
 }
@@ -339,9 +433,38 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* pv, cons
 
 static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Chunks of 512 elements per row for the wave-per-row norms (0 = use the
+// block-per-row kernels): 16-byte aligned rows of fp16 / bf16, dim <= 8192.
+static int norm_chunks(int act, uint32_t dim, std::initializer_list<std::pair<const void*, uint32_t>> rows_) {
+    if (act == LSSM_F32 || dim % 8 != 0 || dim > 8192) return 0;
+    for (auto& r : rows_)
+        if ((uintptr_t)r.first % 16 != 0 || r.second % 8 != 0) return 0;
+    const uint32_t n = (dim + 511) / 512;
+    return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : n <= 8 ? 8 : 16;
+}
+
+#define LSSM_NCH_DISPATCH(nch, NCH, ...)                            \
+    switch (nch) {                                                  \
+        case 1: { constexpr int NCH = 1; __VA_ARGS__; break; }      \
+        case 2: { constexpr int NCH = 2; __VA_ARGS__; break; }      \
+        case 4: { constexpr int NCH = 4; __VA_ARGS__; break; }      \
+        case 8: { constexpr int NCH = 8; __VA_ARGS__; break; }      \
+        default: { constexpr int NCH = 16; __VA_ARGS__; break; }    \
+    }
+
 hipError_t launch_rmsnorm(hipStream_t s, const void* x, uint32_t xs, const void* w, void* y,
                           uint32_t ys, uint32_t rows, uint32_t dim, float eps, int act) {
     if (rows == 0) return hipSuccess;
+    if (const int nch = norm_chunks(act, dim, {{x, xs}, {w, 8}, {y, ys}})) {
+        if (act == LSSM_F16) {
+            LSSM_NCH_DISPATCH(nch, NCH, rmsnorm_wave_kernel<f16, NCH><<<cdiv(rows, 4), 256, 0, s>>>(
+                (const f16*)x, xs, (const f16*)w, (f16*)y, ys, rows, dim, eps));
+        } else {
+            LSSM_NCH_DISPATCH(nch, NCH, rmsnorm_wave_kernel<bf16, NCH><<<cdiv(rows, 4), 256, 0, s>>>(
+                (const bf16*)x, xs, (const bf16*)w, (bf16*)y, ys, rows, dim, eps));
+        }
+        return hipGetLastError();
+    }
     LSSM_DISPATCH_ACT(act, T,
                       rmsnorm_kernel<T><<<rows, NT, 0, s>>>((const T*)x, xs, (const T*)w, (T*)y, ys,
                                                             dim, eps));
@@ -352,6 +475,16 @@ hipError_t launch_gated_rmsnorm(hipStream_t s, const void* z, uint32_t zs, const
                                 uint32_t yst, const void* w, void* out, uint32_t rows, uint32_t dim,
                                 float eps, int act) {
     if (rows == 0) return hipSuccess;
+    if (const int nch = norm_chunks(act, dim, {{z, zs}, {y, yst}, {w, 8}, {out, dim}})) {
+        if (act == LSSM_F16) {
+            LSSM_NCH_DISPATCH(nch, NCH, gated_rmsnorm_wave_kernel<f16, NCH><<<cdiv(rows, 4), 256, 0, s>>>(
+                (const f16*)z, zs, (const f16*)y, yst, (const f16*)w, (f16*)out, rows, dim, eps));
+        } else {
+            LSSM_NCH_DISPATCH(nch, NCH, gated_rmsnorm_wave_kernel<bf16, NCH><<<cdiv(rows, 4), 256, 0, s>>>(
+                (const bf16*)z, zs, (const bf16*)y, yst, (const bf16*)w, (bf16*)out, rows, dim, eps));
+        }
+        return hipGetLastError();
+    }
     LSSM_DISPATCH_ACT(act, T,
                       gated_rmsnorm_kernel<T><<<rows, NT, 0, s>>>((const T*)z, zs, (const T*)y, yst,
                                                                   (const T*)w, (T*)out, dim, eps));

@@ -191,10 +191,13 @@ def test_reference_named_linear_entries(ctx, rng):
 
 
 # --------------------------------------------------------------------------- norms / activations
+# dims: partial 512-element chunks (1536, 40), the 2.7B / 8B widths, and one
+# past the wave-per-row kernels' limit (block-per-row kernels)
 @pytest.mark.parametrize("act", ACTS)
-def test_rmsnorm_and_gated(ctx, rng, act):
+@pytest.mark.parametrize("dim", [1536, 40, 5120, 8192, 8200])
+def test_rmsnorm_and_gated(ctx, rng, act, dim):
     L = _lib()
-    rows, dim = 7, 1536
+    rows = 7
     x = O.to_act(rng.standard_normal((rows, dim)) * 2, act)
     z = O.to_act(rng.standard_normal((rows, dim)), act)
     w = O.to_act(1 + 0.1 * rng.standard_normal(dim), act)
