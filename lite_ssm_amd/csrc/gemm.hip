@@ -229,7 +229,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs a) {
 // elements (128 B) whose 16-byte slots are XOR-swizzled by row % 8, so the
 // fragment reads of 8 consecutive rows hit distinct banks without padding.
 // ---------------------------------------------------------------------------
-constexpr int G2M = 256, G2N = 128, G2K = 64, G2T = 512;
+constexpr int G2M = 256, G2K = 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -306,19 +306,25 @@ template <typename T> __device__ __forceinline__ uint32_t lds_addr(const T* p) {
     return (uint32_t)(size_t)((const __attribute__((address_space(3))) T*)p);
 }
 
-template <int FMT, typename T, int EPI>
-__global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
+// CW compute waves: 4 -> 256 x 128 tile, 8 -> 256 x 256 (quantized W only:
+// the LDS is then exactly full, 3 x 32 KiB of X + 2 x 32 KiB of W).
+template <int FMT, typename T, int EPI, int CW>
+__global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
     constexpr bool DENSE = FMT == LSSM_W_DENSE;
+    static_assert(CW == 4 || (CW == 8 && !DENSE), "tile");
+    constexpr int BN = 32 * CW;                   // tile columns (rows of W)
     constexpr int SB = DENSE ? 3 : 2;             // W stages (dense W also goes by DMA)
+    constexpr int XR = G2M / CW;                  // X rows each compute wave loads
+    constexpr bool DB = CW == 4;                  // fragments double-buffered (registers allow)
     __shared__ __attribute__((aligned(16))) T As[3][G2M * G2K];
-    __shared__ __attribute__((aligned(16))) T Bs[SB][G2N * G2K];
+    __shared__ __attribute__((aligned(16))) T Bs[SB][BN * G2K];
     using Op = MfmaOp<T>;
     using frag = typename Op::frag;
 
     const int t = threadIdx.x;
     const int lane = t % WAVE;
     const int w = __builtin_amdgcn_readfirstlane(t / WAVE);
-    const uint32_t m0 = blockIdx.y * G2M, n0 = blockIdx.x * G2N;
+    const uint32_t m0 = blockIdx.y * G2M, n0 = blockIdx.x * BN;
     const uint32_t K = a.K, KT = K / G2K;
     // a barrier without __syncthreads' release fence (which would wait for
     // every DMA in flight); the empty asm keeps memory operations in place
@@ -328,10 +334,10 @@ __global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
         asm volatile("" ::: "memory");
     };
 
-    if (w >= 4) {
-        // ---------------- producers: waves 4..7, W only ----------------
-        const int q = w - 4;
-        const uint32_t p = t - 256;
+    if (w >= CW) {
+        // ---------------- producers: the last 4 waves, W only ----------------
+        const int q = w - CW;
+        const uint32_t p = t - 64 * CW;
         if constexpr (DENSE) {
             // by DMA: producer wave q fills tile rows 32 q .. + 32, 8 rows per
             // instruction (lane i: row + i / 8, physical slot i % 8 = logical
@@ -361,38 +367,39 @@ __global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
             __builtin_amdgcn_s_waitcnt(0x0F70);
             return;
         } else {
-            // thread p owns row p / 2 of the tile, weights (p % 2) * 32 .. + 32
-            // of a step; step k + 2's are loaded into registers at the start
-            // of step k (two register sets) and dequantized into LDS in step
-            // k + 1.
-            const uint32_t br = p / 2, bh = p % 2;
+            // thread p owns row p / TPR of the tile and CPT chunks of 16 k of
+            // a step (BN = 128: half a row, BN = 256: a whole row); step k +
+            // 2's are loaded into registers at the start of step k (two
+            // register sets) and dequantized into LDS in step k + 1.
+            constexpr int CPT = BN / 64, TPR = 4 / CPT;
+            const uint32_t br = p / TPR, c0 = (p % TPR) * CPT;
             constexpr uint32_t GS = FMT == LSSM_W_Q4_G64 ? 64 : 32;
             const uint32_t nrow = min(n0 + br, a.N - 1);
             const char* wq = (const char*)a.w + (size_t)nrow * (FMT == LSSM_W_Q8_G32 ? K : K / 2);
             const uint16_t* sp = (const uint16_t*)a.s + (size_t)nrow * (K / GS);
             using R = WRaw<FMT>;
-            auto load_w = [&](uint32_t kt, R (&r)[2]) {
+            auto load_w = [&](uint32_t kt, R (&r)[CPT]) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t k = kt * G2K + 32 * bh + 16 * h;
+                for (int h = 0; h < CPT; ++h) {
+                    const uint32_t k = kt * G2K + 16 * (c0 + h);
                     if constexpr (FMT == LSSM_W_Q8_G32) r[h].q = *reinterpret_cast<const u32x4*>(wq + k);
                     else r[h].q = *reinterpret_cast<const u32x2*>(wq + k / 2);
                     r[h].s = sp[k / GS];
                 }
             };
-            auto store_w = [&](uint32_t kt, const R (&r)[2]) {
+            auto store_w = [&](uint32_t kt, const R (&r)[CPT]) {
                 T* Brow = Bs[kt % SB] + br * G2K;
                 const uint32_t sw = br % 8;
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < CPT; ++h) {
                     uint32_t d[8];
                     dequant16<FMT, T>(r[h], d);
-                    const uint32_t s0 = 4 * bh + 2 * h;
+                    const uint32_t s0 = 2 * (c0 + h);
                     *reinterpret_cast<u32x4*>(Brow + 8 * (s0 ^ sw)) = u32x4{d[0], d[1], d[2], d[3]};
                     *reinterpret_cast<u32x4*>(Brow + 8 * ((s0 + 1) ^ sw)) = u32x4{d[4], d[5], d[6], d[7]};
                 }
             };
-            R r0[2], r1[2];
+            R r0[CPT], r1[CPT];
             load_w(0, r0);
             load_w(min(1u, KT - 1), r1);
             store_w(0, r0);
@@ -401,7 +408,7 @@ __global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
             // step kt: load step kt + 2, then write step kt + 1 (its loads were
             // issued a step ago).  Branch-free: past the end it re-loads step
             // KT - 1 and writes the idle stage.
-            auto step = [&](uint32_t kt, R (&ld)[2], const R (&wr)[2]) {
+            auto step = [&](uint32_t kt, R (&ld)[CPT], const R (&wr)[CPT]) {
                 load_w(min(kt + 2, KT - 1), ld);
                 __builtin_amdgcn_sched_barrier(0);    // loads first
                 store_w(kt + 1, wr);
@@ -418,19 +425,20 @@ __global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
         }
     }
 
-    // ---------------- consumers: waves 0..3, 128 x 64 of Y each ----------------
-    // They also DMA X: wave c fills tile rows 64 c .. + 64 of the stage two
+    // ---------------- compute waves: 128 x 64 of Y each ----------------
+    // They also DMA X: wave c fills tile rows XR c .. + XR of the stage two
     // steps ahead, 8 rows per instruction (lane i: row + i / 8, physical slot
     // i % 8 = logical slot (i % 8) ^ (i / 8)); rows past M re-read row M - 1.
-    const int wm = w / 2, wn = w % 2;
+    const int wm = w / (CW / 2), wn = w % (CW / 2);
     const uint32_t xl = (lane % 8) ^ (lane / 8);
-    uint32_t xo[8];
+    constexpr int XJ = XR / 8;                    // DMA instructions per step
+    uint32_t xo[XJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t m = min(m0 + 64 * w + 8 * j + lane / 8, a.M - 1);
+    for (int j = 0; j < XJ; ++j) {
+        const uint32_t m = min(m0 + XR * w + 8 * j + lane / 8, a.M - 1);
         xo[j] = (m * a.x_stride + 8 * xl) * (uint32_t)sizeof(T);
     }
-    const uint32_t as0 = lds_addr(&As[0][0]) + (64 * w) * G2K * (uint32_t)sizeof(T);
+    const uint32_t as0 = lds_addr(&As[0][0]) + (XR * w) * G2K * (uint32_t)sizeof(T);
     auto dma_x = [&](uint32_t kt, int j0, int j1) {
         const char* base = (const char*)a.x + (size_t)kt * G2K * sizeof(T);
         const uint32_t dst = as0 + (kt % 3) * (G2M * G2K * (uint32_t)sizeof(T));
@@ -449,39 +457,53 @@ __global__ __launch_bounds__(G2T) void gemm2_kernel(GemmArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) fo[ks] = (lane % 32) * G2K + 8 * ((2 * ks + lane / 32) ^ (lane % 8));
 
-    // 8 DMAs per step: vmcnt(8) = the previous step's are done
-    dma_x(0, 0, 8);
-    dma_x(min(1u, KT - 1), 0, 8);
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    // XJ DMAs per step: vmcnt(XJ) = the previous step's are done
+    auto wait_prev = [] {
+        if constexpr (XJ == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    };
+    dma_x(0, 0, XJ);
+    dma_x(min(1u, KT - 1), 0, XJ);
+    wait_prev();
     barrier();                                    // step 0 in LDS
     for (uint32_t kt = 0; kt < KT; ++kt) {
         const T* Ab = As[kt % 3] + (wm * 128) * G2K;
         const T* Bb = Bs[kt % SB] + (wn * 64) * G2K;
         const uint32_t k2 = min(kt + 2, KT - 1);
-        frag af[2][4], bfr[2][2];
+        frag af[DB ? 2 : 1][4], bfr[DB ? 2 : 1][2];
         auto rd = [&](int ks, frag (&fa)[4], frag (&fb)[2]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const frag*>(Ab + 32 * i * G2K + fo[ks]);
 #pragma unroll
             for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const frag*>(Bb + 32 * j * G2K + fo[ks]);
         };
-        rd(0, af[0], bfr[0]);
+        if constexpr (DB) rd(0, af[0], bfr[0]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            if (ks + 1 < 4) rd(ks + 1, af[(ks + 1) % 2], bfr[(ks + 1) % 2]);
+            const int cb = DB ? ks % 2 : 0;
+            if constexpr (DB) {
+                if (ks + 1 < 4) rd(ks + 1, af[(ks + 1) % 2], bfr[(ks + 1) % 2]);
+            } else {
+                // two compute waves per SIMD hide the LDS latency instead
+                rd(ks, af[0], bfr[0]);
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(af[ks % 2][i], bfr[ks % 2][j], acc[i][j]);
-            // next sub-step's fragment reads ahead of this sub-step's MFMAs
-            // (the asm DMA below ends the scheduling region)
-            if (ks == 0) __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
-            else if (ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-            dma_x(k2, 2 * ks, 2 * ks + 2);        // step kt + 2's X, 2 runs per sub-step
+                for (int j = 0; j < 2; ++j) acc[i][j] = Op::mma(af[cb][i], bfr[cb][j], acc[i][j]);
+            if constexpr (DB) {
+                // next sub-step's fragment reads ahead of this sub-step's
+                // MFMAs (the asm DMA below ends the scheduling region)
+                if (ks == 0) __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+                else if (ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            }
+            // step kt + 2's X, spread over the sub-steps
+            dma_x(k2, ks * XJ / 4, (ks + 1) * XJ / 4);
         }
         // step kt + 1's X in LDS, this step's fragment reads done
-        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+        if constexpr (XJ == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
         barrier();
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -721,11 +743,26 @@ hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
     // the large tile for prefill-sized M; X byte offsets within a 256-row
     // tile fit 32 bits
     if (a.M > 128 && (uint64_t)a.M * a.x_stride * sizeof(T) < (1ull << 31)) {
-        dim3 grid((a.N + G2N - 1) / G2N, (a.M + G2M - 1) / G2M);
+        // 256-wide tiles halve the X re-reads; worth it when they still give
+        // whole rounds of blocks (>= 3 blocks per CU)
+        const uint32_t mt = (a.M + G2M - 1) / G2M;
+        const bool wide = FMT != LSSM_W_DENSE && (size_t)mt * ((a.N + 255) / 256) >= 3 * (size_t)num_cus();
+        if (wide) {
+            dim3 grid((a.N + 255) / 256, mt);
+            if constexpr (FMT != LSSM_W_DENSE) {
+                switch (a.epi) {
+                    case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU, 8><<<grid, 768, 0, s>>>(a); break;
+                    case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD, 8><<<grid, 768, 0, s>>>(a); break;
+                    default: gemm2_kernel<FMT, T, LSSM_EPI_NONE, 8><<<grid, 768, 0, s>>>(a); break;
+                }
+            }
+            return hipGetLastError();
+        }
+        dim3 grid((a.N + 127) / 128, mt);
         switch (a.epi) {
-            case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU><<<grid, G2T, 0, s>>>(a); break;
-            case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD><<<grid, G2T, 0, s>>>(a); break;
-            default: gemm2_kernel<FMT, T, LSSM_EPI_NONE><<<grid, G2T, 0, s>>>(a); break;
+            case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU, 4><<<grid, 512, 0, s>>>(a); break;
+            case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD, 4><<<grid, 512, 0, s>>>(a); break;
+            default: gemm2_kernel<FMT, T, LSSM_EPI_NONE, 4><<<grid, 512, 0, s>>>(a); break;
         }
         return hipGetLastError();
     }

@@ -103,6 +103,19 @@ def test_gemm_decode_batch_epilogues(ctx, rng, act):
     assert_close(act_host(ys, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2}[act], "silu")
 
 
+@pytest.mark.parametrize("wfmt", QFMTS)
+def test_gemm_wide_tiles(ctx, rng, wfmt):
+    """Enough 256 x 256 tiles for the wide GEMM (>= 3 per CU on 256 CUs), with
+    partial last tiles in M and N and an odd number of K steps."""
+    act, M, N, K = O.BF16, 2000, 24500, 192
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    y = empty((M, N), act)
+    ctx.linear(dev(x), dev(w), dev(s), y, M, N, K, wfmt, act)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, round_dequant=1)
+    assert_close(act_host(y, act), ref, act, 1.6e-2, "gemm")
+
+
 @pytest.mark.parametrize("wfmt", [O.W_Q4_G64, O.W_Q8_G32, O.W_DENSE])
 @pytest.mark.parametrize("K", [64, 192])
 def test_gemm_one_and_odd_k_steps(ctx, rng, wfmt, K):
