@@ -306,6 +306,19 @@ template <typename T> __device__ __forceinline__ uint32_t lds_addr(const T* p) {
     return (uint32_t)(size_t)((const __attribute__((address_space(3))) T*)p);
 }
 
+// Workgroups go to the 8 XCDs round-robin in launch order (linear id % 8),
+// and each XCD has its own L2.  Give XCD x a contiguous run of the tiles in
+// M-major order, so the blocks that share an X row block (all N tiles of one
+// M tile) run on one XCD and read X through one L2.  A bijection for any grid.
+__device__ __forceinline__ void xcd_tile(uint32_t& mt, uint32_t& nt) {
+    const uint32_t nbx = gridDim.x, total = nbx * gridDim.y;
+    const uint32_t lin = blockIdx.x + nbx * blockIdx.y;
+    const uint32_t x = lin % 8, q = total / 8, r = total % 8;
+    const uint32_t tile = x * q + min(x, r) + lin / 8;
+    mt = tile / nbx;
+    nt = tile % nbx;
+}
+
 // CW compute waves: 4 -> 256 x 128 tile, 8 -> 256 x 256 (quantized W only:
 // the LDS is then exactly full, 3 x 32 KiB of X + 2 x 32 KiB of W).
 template <int FMT, typename T, int EPI, int CW>
@@ -324,7 +337,9 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
     const int t = threadIdx.x;
     const int lane = t % WAVE;
     const int w = __builtin_amdgcn_readfirstlane(t / WAVE);
-    const uint32_t m0 = blockIdx.y * G2M, n0 = blockIdx.x * BN;
+    uint32_t tm, tn;
+    xcd_tile(tm, tn);
+    const uint32_t m0 = tm * G2M, n0 = tn * BN;
     const uint32_t K = a.K, KT = K / G2K;
     // a barrier without __syncthreads' release fence (which would wait for
     // every DMA in flight); the empty asm keeps memory operations in place
@@ -743,10 +758,15 @@ hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
     // the large tile for prefill-sized M; X byte offsets within a 256-row
     // tile fit 32 bits
     if (a.M > 128 && (uint64_t)a.M * a.x_stride * sizeof(T) < (1ull << 31)) {
-        // 256-wide tiles halve the X re-reads; worth it when they still give
-        // whole rounds of blocks (>= 3 blocks per CU)
+        // 256-wide tiles halve the X re-reads: a wide tile takes about 1.5x
+        // the time of a 128-wide one (measured at the 2.7B out_proj shape),
+        // so take them when their rounds of blocks (one block per CU) cost
+        // less: 1.5 ceil(wide tiles / CUs) <= ceil(narrow tiles / CUs)
         const uint32_t mt = (a.M + G2M - 1) / G2M;
-        const bool wide = FMT != LSSM_W_DENSE && (size_t)mt * ((a.N + 255) / 256) >= 3 * (size_t)num_cus();
+        const size_t cus = num_cus();
+        const size_t rw = (mt * (size_t)((a.N + 255) / 256) + cus - 1) / cus;
+        const size_t rn = (mt * (size_t)((a.N + 127) / 128) + cus - 1) / cus;
+        const bool wide = FMT != LSSM_W_DENSE && 3 * rw <= 2 * rn;
         if (wide) {
             dim3 grid((a.N + 255) / 256, mt);
             if constexpr (FMT != LSSM_W_DENSE) {
