@@ -19,15 +19,18 @@ namespace lssm {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Decode step.  Block (h * PS + ps, b), 256 threads, owns 32 rows p of one
-// head's (P, N) fp32 state: 8 lanes per row, each streaming F = N / 32 float4
-// of state.  Every load is issued first and unconditionally (state, the
-// lane's B and C vectors, then the per-row / per-head scalars as raw bits), so
-// nothing waits before the math; the 8 lanes of a row reduce C.s with
-// shuffles.  2.7B at batch 1: 160 blocks, 4 x 16-byte state loads per thread.
+// Decode step.  Block (h * PS + ps, b), one wave, owns 8 rows p of one head's
+// (P, N) fp32 state: 8 lanes per row, each streaming F = N / 32 float4 of
+// state.  Every load is issued first and unconditionally (state, the lane's B
+// and C vectors, then the per-row / per-head scalars as raw bits), so nothing
+// waits before the math; the 8 lanes of a row reduce C.s with shuffles.
+// 2.7B at batch 1: 640 one-wave blocks (every CU streams part of the state;
+// 256-thread blocks left 96 CUs idle and took 4.96 us instead of 4.08 us),
+// 4 x 16-byte state loads per thread.
 // ---------------------------------------------------------------------------
 constexpr int ST_NV = 8;                              // lanes per state row
-constexpr int ST_RB = 256 / ST_NV;                    // rows per block
+constexpr int ST_NT = 64;                             // threads per block (one wave)
+constexpr int ST_RB = ST_NT / ST_NV;                  // rows per block
 
 template <typename T> __device__ __forceinline__ uint32_t raw_of(const T* p) {
     if constexpr (sizeof(T) == 2) return *reinterpret_cast<const uint16_t*>(p);
@@ -39,7 +42,7 @@ template <typename T> __device__ __forceinline__ float f_of(uint32_t r) {
 }
 
 template <typename T, int F, bool GATE>
-__global__ __launch_bounds__(256) void ssd_step_kernel(SsdArgs a) {
+__global__ __launch_bounds__(ST_NT) void ssd_step_kernel(SsdArgs a) {
     typedef T T4 __attribute__((ext_vector_type(4)));
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     const uint32_t P = a.P, N = a.N;
@@ -559,10 +562,10 @@ hipError_t step_go(hipStream_t s, const SsdArgs& a) {
     const bool vec = ((uintptr_t)a.state % 16 == 0) && ((uintptr_t)a.B % v4 == 0) &&
                      ((uintptr_t)a.C % v4 == 0) && (a.b_stride % 4 == 0) && (a.c_stride % 4 == 0);
     const dim3 grid(a.H * ((a.P + ST_RB - 1) / ST_RB), a.batch);
-    if (vec && a.N == 128) ssd_step_kernel<T, 4, GATE><<<grid, 256, 0, s>>>(a);
-    else if (vec && a.N == 64) ssd_step_kernel<T, 2, GATE><<<grid, 256, 0, s>>>(a);
-    else if (vec && a.N == 256) ssd_step_kernel<T, 8, GATE><<<grid, 256, 0, s>>>(a);
-    else if (vec && a.N == 32) ssd_step_kernel<T, 1, GATE><<<grid, 256, 0, s>>>(a);
+    if (vec && a.N == 128) ssd_step_kernel<T, 4, GATE><<<grid, ST_NT, 0, s>>>(a);
+    else if (vec && a.N == 64) ssd_step_kernel<T, 2, GATE><<<grid, ST_NT, 0, s>>>(a);
+    else if (vec && a.N == 256) ssd_step_kernel<T, 8, GATE><<<grid, ST_NT, 0, s>>>(a);
+    else if (vec && a.N == 32) ssd_step_kernel<T, 1, GATE><<<grid, ST_NT, 0, s>>>(a);
     else ssd_step_generic_kernel<T, GATE><<<dim3(a.H, a.batch), ((a.P + 63) / 64) * 64, 0, s>>>(a);
     return hipGetLastError();
 }
