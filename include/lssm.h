@@ -213,6 +213,17 @@ int lssm_linear(lssm_ctx* ctx, const void* x, uint32_t x_stride,
                 uint32_t M, uint32_t N, uint32_t K,
                 lssm_wfmt wfmt, lssm_dtype act, lssm_epilogue epi);
 
+/* Decode linear with the RMSNorm prologue, for 1..64 rows (one token of each
+ * of `rows` sequences): y = epi(r(RMSNorm(x, norm_w, eps)) . deq(W)^T) with
+ * the GEMV rule at every row count (exact dequantization, linear.metal:440-474),
+ * as the reference decodes each sequence (mamba2_block.cpp:240-262: rmsnorm ->
+ * linear gemv -> add_inplace; the engine's out_proj step).  `residual` may
+ * alias `y` (EPI_ADD).  Rows are packed (stride K in, N out). */
+int lssm_norm_linear_decode(lssm_ctx* ctx, const void* x, const void* norm_w, float eps,
+                            const void* w, const void* w_scales, void* y, const void* residual,
+                            uint32_t rows, uint32_t N, uint32_t K, lssm_wfmt wfmt,
+                            lssm_dtype act, lssm_epilogue epi);
+
 /* Bit-exact dequantization of a whole (N x K) weight into fp32 (debug/parity). */
 int lssm_dequant(lssm_ctx* ctx, const void* w, const void* w_scales, float* out,
                  uint32_t N, uint32_t K, lssm_wfmt wfmt);
@@ -254,7 +265,7 @@ int lssm_ssd_step(lssm_ctx* ctx, const void* x, const void* B, const void* C,
                   const void* D_skip, float* state, void* y, uint32_t batch,
                   lssm_ssd_step_dims dims, lssm_dtype act);
 
-/* Fused decode in_proj for batch <= 4 rows (the engine's first kernel of a
+/* Fused decode in_proj for batch <= 64 rows (the engine's first kernel of a
  * layer): normed = r(RMSNorm(hidden, norm_w)); proj = r(normed . deq(W)^T) over
  * all [z | xBC | dt] rows; z and dt rows are stored, each xBC row goes through
  * the conv-window update (conv1d.metal:108-137) and r(SiLU(r(conv))) into

@@ -137,6 +137,7 @@ _SIGS = {
     "lssm_conv1d_update": ([_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i], _i),
     "lssm_conv1d_seed": ([_vp, _vp, _vp, _u32, _u32, _u32, _u32, _i], _i),
     "lssm_gated_rmsnorm": ([_vp, _vp, _vp, _vp, _vp, _u32, _u32, _f, _i], _i),
+    "lssm_norm_linear_decode": ([_vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _i, _i], _i),
     "lssm_ssd_chunked": ([_vp] + [_vp] * 9 + [_u32, SSDDims, _i], _i),
     "lssm_ssd_step": ([_vp] + [_vp] * 9 + [_u32, SSDStepDims, _i], _i),
     "lssm_inproj_decode": ([_vp] * 11 + [_u32] * 7 + [_f, _i, _i], _i),

@@ -106,6 +106,26 @@ int lssm_linear(lssm_ctx* ctx, const void* x, uint32_t x_stride, const void* w, 
                        0, "linear");
 }
 
+int lssm_norm_linear_decode(lssm_ctx* ctx, const void* x, const void* norm_w, float eps,
+                            const void* w, const void* w_scales, void* y, const void* residual,
+                            uint32_t rows, uint32_t N, uint32_t K, lssm_wfmt wfmt,
+                            lssm_dtype act, lssm_epilogue epi) {
+    LSSM_CHECK_CTX(ctx);
+    LSSM_REQUIRE(valid_act(act), "norm_linear_decode: unknown dtype");
+    if (int rc = check_fmt_k(K, wfmt, w_scales)) return rc;
+    LSSM_REQUIRE(epi == LSSM_EPI_NONE || epi == LSSM_EPI_SILU || epi == LSSM_EPI_ADD,
+                 "norm_linear_decode: unknown epilogue %d", (int)epi);
+    LSSM_REQUIRE(epi != LSSM_EPI_ADD || residual != nullptr, "norm_linear_decode: EPI_ADD needs a residual");
+    LSSM_REQUIRE(rows <= 64, "norm_linear_decode: rows must be <= 64");
+    if (rows == 0 || N == 0) return LSSM_OK;
+    LSSM_REQUIRE(x && norm_w && w && y, "norm_linear_decode: null pointer");
+    LSSM_REQUIRE(gemv_ok(w, K, wfmt, act), "norm_linear_decode: unsupported K / weight alignment");
+    GemvArgs g{x, K, w, w_scales, y, N, residual, norm_w, eps, rows, N, K, wfmt, act, epi};
+    hipError_t e = launch_gemv(ctx->stream, g);
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "norm_linear_decode: %s", hipGetErrorString(e));
+    return finish(ctx, "norm_linear_decode");
+}
+
 int lssm_dequant(lssm_ctx* ctx, const void* w, const void* w_scales, float* out, uint32_t N,
                  uint32_t K, lssm_wfmt wfmt) {
     LSSM_CHECK_CTX(ctx);
@@ -240,12 +260,12 @@ int lssm_inproj_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, co
     LSSM_CHECK_CTX(ctx);
     LSSM_REQUIRE(valid_act(act), "inproj_decode: unknown dtype");
     if (int rc = check_fmt_k(d_model, wfmt, w_scales)) return rc;
-    LSSM_REQUIRE(batch >= 1 && batch <= 4, "inproj_decode: batch must be in [1, 4]");
+    LSSM_REQUIRE(batch >= 1 && batch <= 64, "inproj_decode: batch must be in [1, 64]");
     LSSM_REQUIRE(d_conv >= 1, "inproj_decode: d_conv must be >= 1");
     LSSM_REQUIRE((uintptr_t)conv_state % 8 == 0 && (uintptr_t)conv_w % 8 == 0,
                  "inproj_decode: conv_state and conv_w must be 8-byte aligned");
     LSSM_REQUIRE(gemv_ok(w, d_model, wfmt, act), "inproj_decode: unsupported d_model / weight alignment");
-    LSSM_REQUIRE((int)batch <= gemv_max_rows(d_model, wfmt, act), "inproj_decode: batch * d_model too large");
+    LSSM_REQUIRE(gemv_max_rows(d_model, wfmt, act) >= 1, "inproj_decode: d_model too large");
     const uint32_t xbc = d_inner + 2u * n_groups * d_state;
     InprojDecodeArgs a;
     a.g = GemvArgs{hidden, d_model, w, w_scales, nullptr, 0, nullptr, norm_w, eps, batch,

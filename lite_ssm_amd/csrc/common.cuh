@@ -53,19 +53,38 @@ __device__ __forceinline__ float fp16_bits_to_f(uint16_t b) {
     return (float)c.h;
 }
 
-// Sum over a full 64-lane wave; result in every lane.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
+// Lane sums without LDS round trips: DPP within 16-lane rows (quad perms,
+// half-row and row mirrors), then the gfx950 row-swap permutes across rows.
+// Every step adds two partial sums that some other lane adds in the other
+// order (fp32 addition commutes), so all lanes of a group end with the same
+// bits, and the order of the additions is fixed (deterministic).
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float swap_add16(float v) {           // rows 2j, 2j+1
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float swap_add32(float v) {           // lane halves
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Sum over aligned groups of `W` lanes (W a power of two <= 64); the result in
+// every lane of the group.
+template <int W> __device__ __forceinline__ float group_sum(float v) {
+    static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group");
+    if constexpr (W >= 2) v += dpp_f32<0xB1>(v);                 // quad_perm 1,0,3,2
+    if constexpr (W >= 4) v += dpp_f32<0x4E>(v);                 // quad_perm 2,3,0,1
+    if constexpr (W >= 8) v += dpp_f32<0x141>(v);                // row_half_mirror
+    if constexpr (W >= 16) v += dpp_f32<0x140>(v);               // row_mirror
+    if constexpr (W >= 32) v = swap_add16(v);
+    if constexpr (W >= 64) v = swap_add32(v);
     return v;
 }
 
-// Sum over aligned groups of `W` lanes (W a power of two <= 64).
-template <int W> __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = W / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
-    return v;
-}
+// Sum over a full 64-lane wave; result in every lane.
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<WAVE>(v); }
 
 // Block-wide sum for blockDim.x == NT threads; `red` is >= NT/64 floats of LDS.
 template <int NT> __device__ __forceinline__ float block_sum(float v, float* red) {

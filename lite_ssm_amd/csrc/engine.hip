@@ -87,10 +87,13 @@ struct lssm_engine {
 
     hipStream_t st() const { return ctx->stream; }
 
-    // Linear on the fastest kernel for the shape (GEMV for M <= 4).
+    // Decode-side linear (one token per sequence): quantized weights keep the
+    // GEMV rule at any batch, as the reference's decode (mamba2_block.cpp:111,
+    // 248: decode || L == 1 -> gemv) does per sequence; dense weights take the
+    // GEMM kernels above 4 rows (the same arithmetic).
     hipError_t linear(const void* x, uint32_t xs, const void* w, const void* s, void* y, uint32_t ysd,
                       const void* res, uint32_t M, uint32_t Nn, uint32_t Kk, int fmt, int epi) const {
-        if (M <= 4) {
+        if (M <= 4 || fmt != LSSM_W_DENSE) {
             GemvArgs g{x, xs, w, s, y, ysd, res, nullptr, 0.0f, M, Nn, Kk, fmt, act, epi};
             return launch_gemv(st(), g);
         }
@@ -119,8 +122,12 @@ struct lssm_engine {
     // One decode step: ids -> next (all on device).  mamba2_block.cpp:317-327.
     hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
         hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act);
-        const bool fused_in = B <= 4 && (int)B <= gemv_max_rows(d_model, wfmt, act);
-        const bool fused_out = B <= 4 && gemv_max_rows(d_inner, wfmt, act) >= 1;
+        // fused RMSNorm + linear kernels: the VALU GEMV up to 4 rows, the MFMA
+        // GEMV for decode batches of the shapes it takes
+        const bool fused_in = (B <= 4 && (int)B <= gemv_max_rows(d_model, wfmt, act)) ||
+                              (B >= 2 && gemv_mma_takes(B, proj, d_model, wfmt, act));
+        const bool fused_out = (B <= 4 && gemv_max_rows(d_inner, wfmt, act) >= 1) ||
+                               (B >= 2 && gemv_mma_takes(B, d_model, d_inner, wfmt, act));
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
             char* cs = conv_layer(li);

@@ -1,0 +1,630 @@
+// gemv_mma.hip — decode batches of 2..64 rows on MFMA with the GEMV rule
+// (exact dequantization, linear.metal:440-474), RMSNorm prologue and the
+// per-row epilogues of gemv.hip fused.
+#include <algorithm>
+
+#include "gemv_core.cuh"
+
+namespace lssm {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// gemv_mma: decode batches (2..64 rows of x) on v_mfma_f32_16x16x32, GEMV rule
+// ---------------------------------------------------------------------------
+// y[m, n] = epi(sum_g s[n, g] * sum_{k in g} q[n, k] x[m, k]): the unpacked
+// integers (136 + q for int4 x bf16, whose 136 * sum(x) per group is taken off
+// again; exact q otherwise) are the MFMA operands and each group's fp32 sum is
+// scaled once, so no weight is rounded (linear.metal:440-474), as in gemv1.
+//
+// A block owns CT tiles of 16 W rows; its KS waves split K into whole quads
+// (QK = 4 chunks of one row: one 16-byte load by each of the row's 4 lanes),
+// QPW quads per wave.  MFMA operands: A = x (16 batch rows), B = W (16 W rows
+// as columns); lane l = 16 q + i supplies row i and k-slice q (8 values) of an
+// MFMA's 32, and holds D rows 4 q .. 4 q + 3 (batch) of column i (W row) after
+// it.  An MFMA must stay inside one scale group, so after the load the 4 lanes
+// of a row trade dwords (v_permlane32_swap for 64-wide groups, and then
+// v_permlane16_swap for 32-wide ones) until each k-slice a lane supplies lies
+// in one group; x is read from LDS in the matching order.
+//
+// x rows [base, base + mpb) are staged per pass, RMSNorm'ed when fused
+// (norm.metal:52-79: r((x w) rrms), rrms = 1 / sqrt(mean(x^2) + eps)), in LDS
+// as the packed pairs of the weight unpack (pair_pos order, row pitch K/2 + 4
+// dwords: the 16-byte reads of 8 consecutive rows fall in distinct banks),
+// plus each group's sum(x) for the int4 x bf16 bias.  More rows than fit take
+// further passes over the same weights, which stay in registers.  The weights
+// are requested after the staging barrier: x is not queued behind them.  The
+// KS partial sums meet in LDS, summed in wave order (deterministic); wave t
+// finishes tile t through the epilogue.
+// Waves per block a (tiles, quads per wave) shape is built for: more weight
+// registers per lane, fewer waves (VGPRs per lane: 128 / 168 / 256).
+constexpr int mma_waves(int ct, int qpw) { return ct * qpw <= 2 ? 16 : (ct * qpw <= 8 ? 12 : 8); }
+// The instantiated shapes: several tiles per block for int4 only (the large
+// models' formats).
+constexpr bool mma_shape_ok(int ct, int qpw, bool q4) {
+    return (ct == 1 && (qpw == 1 || qpw == 2 || qpw == 4 || qpw == 8)) ||
+           (q4 && ((qpw == 2 && ct >= 2 && ct <= 4) || (ct == 4 && qpw == 4)));
+}
+constexpr int MM_MAXJ = 8;                       // staged octets per thread and pass
+constexpr size_t MM_LDS_MAX = 150 * 1024;        // dynamic LDS (static: < 5 KiB)
+
+template <int V> struct FmtTag {
+    static constexpr int value = V;
+};
+
+template <int FMT, typename T> struct Mma {
+    using F = Fmt<FMT, T>;
+    static constexpr int WPC = F::WPC;
+    static constexpr int NP = WPC / 2;                                  // pairs per chunk
+    static constexpr int QK = 4 * WPC;                                  // k per quad
+    static constexpr int G = F::G;                                      // 0: dense
+    static constexpr int SPQ = FMT == LSSM_W_DENSE ? 1 : (FMT == LSSM_W_Q8_G32 ? 2 : 4);  // MFMAs per quad
+    static constexpr int GPQ = G ? QK / G : 1;                          // scale groups per quad
+    static constexpr int SPG = SPQ / GPQ;                               // MFMAs per group
+    static constexpr bool BIAS = q4_bf16<FMT, T>();
+};
+
+// Chunk (within the quad) and pair offset of MFMA k-slice s of lane group q,
+// after mma_swap: the x pairs that slice s meets in lane group q.
+template <int FMT> __device__ __forceinline__ void mma_slice_pos(int s, int q, int& ch, int& po) {
+    if constexpr (FMT == LSSM_W_Q4_G64) {
+        ch = (q & 1) + 2 * (s >> 1);
+        po = 4 * ((s & 1) + 2 * (q >> 1));
+    } else if constexpr (FMT == LSSM_W_Q4_B32) {
+        ch = s;
+        po = 4 * q;
+    } else if constexpr (FMT == LSSM_W_Q8_G32) {
+        ch = (q & 1) + 2 * s;
+        po = 4 * (q >> 1);
+    } else {
+        ch = q;
+        po = 0;
+    }
+}
+
+// Lane group q loaded chunk q of the quad (dwords C_q[0..3]).  After the
+// 32-lane swap, lane group q holds C_{q&1}[2(q>>1)], C_{q&1}[2(q>>1)+1],
+// C_{(q&1)+2}[2(q>>1)], C_{(q&1)+2}[2(q>>1)+1]: dwords 0-1 come from chunks
+// 0-1 and dwords 2-3 from chunks 2-3 (one 64-wide group each).  After the
+// 16-lane swap as well it holds C_0[q], C_1[q], C_2[q], C_3[q] (dword j from
+// chunk j: one 32-wide group each).
+template <int FMT> __device__ __forceinline__ u32x4 mma_swap(u32x4 v) {
+    if constexpr (FMT == LSSM_W_DENSE) {
+        return v;
+    } else {
+        const auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+        const auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+        u32x4 r = u32x4{a[0], b[0], a[1], b[1]};
+        if constexpr (FMT == LSSM_W_Q4_B32) {
+            const auto c = __builtin_amdgcn_permlane16_swap(r[0], r[1], false, false);
+            const auto d = __builtin_amdgcn_permlane16_swap(r[2], r[3], false, false);
+            r = u32x4{c[0], c[1], d[0], d[1]};
+        }
+        return r;
+    }
+}
+
+// Pair q of an octet (8 consecutive k, 8-aligned) in pair_pos order: the
+// positions (within the octet) of its two values.  Octets never straddle the
+// pair structure of a chunk, so these are constants.
+template <int FMT, typename T> __device__ __forceinline__ void octet_pos(int q, int& a, int& b) {
+    if constexpr (q4_bf16<FMT, T>()) {
+        a = ((q & 2) ? 1 : 0) + ((q & 1) ? 4 : 0);
+        b = a + 2;
+    } else if constexpr (is_q4<FMT>()) {
+        a = q;
+        b = q + 4;
+    } else if constexpr (FMT == LSSM_W_Q8_G32) {
+        a = 4 * (q / 2) + q % 2;
+        b = a + 2;
+    } else {
+        a = 2 * q;
+        b = a + 1;
+    }
+}
+
+// The 8 weights of MFMA k-slice s of a swapped quad as packed pairs: dword s
+// (int4), dwords 2s, 2s+1 (int8), the whole quad chunk (dense).
+template <int FMT, typename T> __device__ __forceinline__ u32x4 unpack_slice(u32x4 v, int s) {
+    if constexpr (FMT == LSSM_W_DENSE) {
+        return v;
+    } else if constexpr (FMT == LSSM_W_Q8_G32) {
+        const Unpacked<FMT, T> u = unpack<FMT, T>(make_uint4(v[2 * s], v[2 * s + 1], 0u, 0u));
+        return u32x4{u.p[0], u.p[1], u.p[2], u.p[3]};
+    } else {
+        const Unpacked<FMT, T> u = unpack<FMT, T>(make_uint4(v[s], 0u, 0u, 0u));
+        return u32x4{u.p[0], u.p[1], u.p[2], u.p[3]};
+    }
+}
+
+template <typename T> __device__ __forceinline__ floatx4 mfma16(u32x4 a, u32x4 b, floatx4 c) {
+    if constexpr (__is_same(T, bf16))
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+
+// ra: dwords of the LDS region that holds, in turn, the lanes' sums of
+// squares, the staged x rows and each pass's partial sums.
+template <int FMT, typename T, int CT, int QPW, bool NORM, class Epi>
+__global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvCore c, Epi epi, uint32_t M, uint32_t mpb,
+                                                                 uint32_t ra) {
+    using P = Mma<FMT, T>;
+    using F = Fmt<FMT, T>;
+    constexpr int NP = P::NP, GPQ = P::GPQ, SPG = P::SPG;
+    constexpr bool BIAS = P::BIAS;
+    extern __shared__ __attribute__((aligned(16))) uint32_t mm_lds[];
+    __shared__ float rinv_s[16];
+
+    const uint32_t K = c.K, N = c.N;
+    const int lane = threadIdx.x % WAVE, li = lane % 16, lq = lane / 16;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    const int KS = blockDim.x / WAVE;
+    const uint32_t RS = K / 2 + 4;                             // x row pitch (dwords)
+    const uint32_t KO = K / 8;                                 // octets per row
+    const uint32_t SEG = (KO + 63) / 64;                       // 64-octet segments per row
+    uint32_t* xl = mm_lds;
+    const uint32_t tiles = (N + 15) / 16;
+    const uint32_t tile0 = blockIdx.x * CT;
+    // A block barrier that waits for this wave's LDS accesses only: the weight
+    // loads in flight are not waited for (__syncthreads' release would).
+    auto lds_barrier = [] {
+        __builtin_amdgcn_s_waitcnt(0xC07F);                    // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // ---- x rows of one pass -> LDS ----
+    // A pass stages mpb rows in segments of 64 octets (8 k each); wave w takes
+    // segments w, w + KS, ... (at most MM_MAXJ), so a segment's row and place
+    // are wave-uniform and a lane's octet is segment * 64 + lane.
+    // KEEP: the x octets stay in registers between the sum of squares and
+    // the normalisation (the first pass, before any weight is in registers);
+    // later passes load them again (cache hits) to keep the registers free.
+    u32x4 xk[MM_MAXJ], nk[MM_MAXJ];                            // the first pass's x octets
+    auto stage = [&](uint32_t base, auto keep) {
+        constexpr bool KEEP = decltype(keep)::value;
+        const uint32_t nseg = mpb * SEG;
+        // the lane index through an empty asm: the addresses below are
+        // recomputed per pass instead of being kept live across the compute
+        uint32_t lane = threadIdx.x % WAVE;
+        asm volatile("" : "+v"(lane));
+        auto load = [&](int j, u32x4& xv, u32x4& nv) {
+            const uint32_t u = w + KS * j;
+            const uint32_t m = min(base + u / SEG, M - 1), cc = min((u % SEG) * 64 + lane, KO - 1);
+            xv = *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(c.x) + (size_t)m * c.x_stride + 8 * cc);
+            if constexpr (NORM) nv = reinterpret_cast<const u32x4*>(c.norm_w)[cc];
+        };
+        if constexpr (NORM) {
+            // sum(x^2) per segment, then 1 / rms per row (segments in order)
+            u32x4 xv[MM_MAXJ];
+#pragma unroll
+            for (int j = 0; j < MM_MAXJ; ++j) {
+                if (w + KS * j < nseg) {
+                    if constexpr (KEEP) {
+                        xv[j] = xk[j];
+                    } else {
+                        u32x4 dummy;
+                        load(j, xv[j], dummy);
+                    }
+                }
+            }
+            // each lane's share in LDS (region A, before x lands there), then
+            // one wave per row sums it in a fixed order
+            float* part = reinterpret_cast<float*>(mm_lds);    // [segment][lane]
+#pragma unroll
+            for (int j = 0; j < MM_MAXJ; ++j) {
+                const uint32_t u = w + KS * j;
+                if (u < nseg) {
+                    const u32x4 d = xv[j];
+                    float q = dot2(d[0], d[0], 0.0f, T{});
+                    q = dot2(d[1], d[1], q, T{});
+                    q = dot2(d[2], d[2], q, T{});
+                    q = dot2(d[3], d[3], q, T{});
+                    part[u * WAVE + lane] = (u % SEG) * 64 + lane < KO ? q : 0.0f;
+                }
+            }
+            lds_barrier();
+            for (uint32_t r = w; r < mpb; r += KS) {
+                float t = 0.0f;
+                for (uint32_t g = 0; g < SEG; ++g) t += part[(r * SEG + g) * WAVE + lane];
+                t = wave_sum(t);
+                if (lane == 0) rinv_s[r] = 1.0f / sqrtf(t / (float)K + c.eps);
+            }
+            lds_barrier();
+        }
+        auto put = [&](int j, const u32x4& xv, const u32x4& nv, float rr) {
+            const uint32_t u = w + KS * j;
+            const uint32_t r = u / SEG, cc = (u % SEG) * 64 + lane;
+            const bool live = cc < KO;
+            float v[8];
+            if constexpr (NORM) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] = dot2(xv[e], nv[e] & 0x0000FFFFu, 0.0f, T{}) * rr;
+                    v[2 * e + 1] = dot2(xv[e], nv[e] & 0xFFFF0000u, 0.0f, T{}) * rr;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] = f_of_bits<T>((uint16_t)(xv[e] & 0xFFFFu));
+                    v[2 * e + 1] = f_of_bits<T>((uint16_t)(xv[e] >> 16));
+                }
+            }
+            u32x4 pk;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int pa, pb;
+                octet_pos<FMT, T>(q, pa, pb);
+                pk[q] = pack2<T>(v[pa], v[pb]);                         // the rounding r()
+            }
+            // the pairs of k .. k + 7 sit at dwords k / 2 .. k / 2 + 3 of the row
+            if (live) *reinterpret_cast<u32x4*>(xl + r * RS + 4 * cc) = pk;
+        };
+        // the rows' 1 / rms first, all at once (one LDS wait, not one per segment)
+        float rr[MM_MAXJ];
+#pragma unroll
+        for (int j = 0; j < MM_MAXJ; ++j) {
+            rr[j] = 1.0f;
+            if constexpr (NORM) {
+                if (w + KS * j < nseg) rr[j] = rinv_s[(w + KS * j) / SEG];
+            }
+        }
+        if constexpr (KEEP) {
+#pragma unroll
+            for (int j = 0; j < MM_MAXJ; ++j)
+                if (w + KS * j < nseg) put(j, xk[j], nk[j], rr[j]);
+        } else {
+            // half of the segments at a time
+#pragma unroll
+            for (int h = 0; h < MM_MAXJ; h += MM_MAXJ / 2) {
+                u32x4 xv[MM_MAXJ / 2], nv[MM_MAXJ / 2];
+#pragma unroll
+                for (int jj = 0; jj < MM_MAXJ / 2; ++jj)
+                    if (w + KS * (h + jj) < nseg) load(h + jj, xv[jj], nv[jj]);
+#pragma unroll
+                for (int jj = 0; jj < MM_MAXJ / 2; ++jj)
+                    if (w + KS * (h + jj) < nseg) put(h + jj, xv[jj], nv[jj], rr[h + jj]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        lds_barrier();
+    };
+
+    // ---- weights (and raw scale bits) of the wave's quads, all in flight ----
+    // With few weight registers (CT * QPW <= 4) they are held over all
+    // passes; otherwise a later pass reads them again (L2 hits) rather than
+    // holding them across its staging.
+    constexpr bool HOLD = CT * QPW <= 4;
+    const size_t rb = F::row_bytes(K);
+    u32x4 wr[CT][QPW];
+    constexpr int SW = (QPW * GPQ + 1) / 2;                    // scale dwords per tile and wave
+    uint32_t sr[CT][SW];
+    auto load_w = [&] {
+    #pragma unroll
+        for (int t = 0; t < CT; ++t) {
+            const uint32_t n = min(16 * (tile0 + t) + li, N - 1);
+    #pragma unroll
+            for (int qd = 0; qd < QPW; ++qd) {
+                const uint32_t qa = w * QPW + qd;
+                wr[t][qd] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(c.w + n * rb + 16 * (4 * qa + lq)));
+            }
+            if constexpr (P::G > 0) {
+                // the wave's QPW * GPQ scales of the row, contiguous (the plan
+                // keeps their offset a multiple of their size)
+                const uint16_t* sp = c.s + n * (K / P::G) + w * QPW * GPQ;
+                if constexpr (SW == 1) {
+                    sr[t][0] = *reinterpret_cast<const uint32_t*>(sp);
+                } else if constexpr (SW == 2) {
+                    const uint2 v = *reinterpret_cast<const uint2*>(sp);
+                    sr[t][0] = v.x;
+                    sr[t][1] = v.y;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < SW / 4; ++i) {
+                        const u32x4 v = *reinterpret_cast<const u32x4*>(sp + 8 * i);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) sr[t][4 * i + e] = v[e];
+                    }
+                }
+            }
+        }
+    };
+    epi.pin();
+    // x of the first pass, staged before any weight is requested: requested
+    // behind the weights, x would queue behind the whole chip's weight
+    // traffic (measured: staging done ~7 us after the start instead of ~2)
+    {
+        const uint32_t nseg = mpb * SEG;
+        const uint32_t lane0 = threadIdx.x % WAVE;
+        // KS a multiple of SEG: every segment of a wave sits at the same place
+        // in its row, so the norm weight is loaded once
+        const bool one_place = KS % SEG == 0;
+#pragma unroll
+        for (int j = 0; j < MM_MAXJ; ++j) {
+            const uint32_t u = w + KS * j;
+            if (u < nseg) {
+                const uint32_t m = min(u / SEG, M - 1), cc = min((u % SEG) * 64 + lane0, KO - 1);
+                xk[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(c.x) + (size_t)m * c.x_stride + 8 * cc);
+                if constexpr (NORM) {
+                    if (j == 0 || !one_place) nk[j] = reinterpret_cast<const u32x4*>(c.norm_w)[cc];
+                    else nk[j] = nk[0];
+                }
+            }
+        }
+    }
+    stage(0u, FmtTag<1>{});
+    load_w();
+
+    for (uint32_t base = 0; base < M; base += mpb) {
+        if (base > 0) {
+            stage(base, FmtTag<0>{});
+            if constexpr (!HOLD) load_w();
+        }
+        const uint32_t rows = min(mpb, M - base);
+        // Epilogue: output element o of the block (tile o / 256, D element o %
+        // 256 as lane * 4 + element) is finished by thread o % NT; its inputs
+        // are requested now.  Element e of lane 16 q + i is batch row 4 q + e,
+        // W row i of the tile.
+        const uint32_t NT = blockDim.x;
+        constexpr int EPT = (CT + 1) / 2;                       // elements per thread (the plan: 64 KS EPT >= 256 CT)
+        typename Epi::Pre pre[EPT];
+        auto out_mn = [&](uint32_t o, uint32_t& m, uint32_t& n) {
+            const uint32_t t = o / 256, l = (o % 256) / 4, e = o % 4;
+            m = base + 4 * (l / 16) + e;
+            n = 16 * (tile0 + t) + l % 16;
+        };
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const uint32_t o = threadIdx.x + NT * k;
+            if (o < CT * 256u) {
+                uint32_t m, n;
+                out_mn(o, m, n);
+                pre[k] = epi.prefetch((int)min(m, M - 1), min(n, N - 1));
+            }
+        }
+        floatx4 acc[CT];
+#pragma unroll
+        for (int t = 0; t < CT; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t xrow = min((uint32_t)li, mpb - 1) * RS;   // A rows past the pass: duplicates
+#pragma unroll
+        for (int qd = 0; qd < QPW; ++qd) {
+            const uint32_t qa = w * QPW + qd;
+            // the 4 lanes of each row trade dwords (one scale group per k-slice);
+            // waits only for this quad's loads
+            u32x4 wq[CT];
+#pragma unroll
+            for (int t = 0; t < CT; ++t) wq[t] = mma_swap<FMT>(wr[t][qd]);
+#pragma unroll
+            for (int g = 0; g < GPQ; ++g) {
+                // x fragments of the group's MFMA k-slices (shared by the CT tiles)
+                u32x4 xf[SPG];
+#pragma unroll
+                for (int e = 0; e < SPG; ++e) {
+                    int ch, po;
+                    mma_slice_pos<FMT>(g * SPG + e, lq, ch, po);
+                    xf[e] = *reinterpret_cast<const u32x4*>(xl + xrow + (4 * qa + ch) * NP + po);
+                }
+                // int4 x bf16: sum(x) of the group's k per batch row, an MFMA
+                // against ones (exact products), shared by the CT tiles
+                floatx4 sxv = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (BIAS) {
+                    constexpr uint32_t ONE2 = 0x3F803F80u;             // bf16 (1, 1)
+#pragma unroll
+                    for (int e = 0; e < SPG; ++e) sxv = mfma16<T>(xf[e], u32x4{ONE2, ONE2, ONE2, ONE2}, sxv);
+                }
+#pragma unroll
+                for (int t = 0; t < CT; ++t) {
+                    // tile by tile: interleaving the tiles' unpacks runs out of registers
+                    if (t > 0) __builtin_amdgcn_sched_barrier(0);
+                    floatx4 d = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int e = 0; e < SPG; ++e) {
+                        const int sl = g * SPG + e;
+                        d = mfma16<T>(xf[e], unpack_slice<FMT, T>(wq[t], sl), P::G == 0 ? acc[t] : d);
+                    }
+                    if constexpr (P::G == 0) {
+                        acc[t] = d;
+                    } else {
+                        const int h = qd * GPQ + g;                         // the scale's half-word
+                        const uint32_t sw = sr[t][h / 2];
+                        const float sc = fp16_bits_to_f((uint16_t)((h & 1) ? sw >> 16 : sw & 0xFFFFu));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float dr = BIAS ? __builtin_fmaf(-136.0f, sxv[r], d[r]) : d[r];
+                            acc[t][r] = __builtin_fmaf(sc, dr, acc[t][r]);
+                        }
+                    }
+                }
+            }
+        }
+        // ---- the KS partial sums of each tile, in wave order ----
+        lds_barrier();                                         // x no longer read
+        floatx4* red = reinterpret_cast<floatx4*>(mm_lds);      // [wave][tile][lane]
+        const float* redf = reinterpret_cast<const float*>(mm_lds);
+#pragma unroll
+        for (int t = 0; t < CT; ++t) red[(w * CT + t) * WAVE + lane] = acc[t];
+        lds_barrier();
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const uint32_t o = threadIdx.x + NT * k;
+            if (o < CT * 256u) {
+                // the KS partial sums in wave order (deterministic)
+                float v = 0.0f;
+                for (int ww = 0; ww < KS; ++ww) v += redf[ww * CT * 256 + o];
+                uint32_t m, n;
+                out_mn(o, m, n);
+                if (m - base < rows && n < N && o / 256 + tile0 < tiles) epi((int)m, n, v, pre[k]);
+            }
+        }
+        lds_barrier();                                         // red read before the next staging
+    }
+}
+
+// ---- gemv_mma launch plan ----
+struct MmaPlan {
+    uint32_t ct = 0, qpw = 0, ks = 0, mpb = 0, ra = 0;
+    size_t lds = 0;
+};
+
+// Quads per wave from {1, 2, 4} (the smallest that splits K into <= 16 waves),
+// tiles per block so that the blocks cover the CUs about once, rows per pass
+// from the LDS budget and the staging registers (<= 8 octets per thread).
+template <int FMT, typename T> bool mma_plan(uint32_t M, uint32_t N, uint32_t K, MmaPlan& p) {
+    using P = Mma<FMT, T>;
+    if (M < 2 || M > 64 || N == 0 || K % P::QK != 0) return false;
+    const uint32_t quads = K / P::QK;
+    constexpr bool q4 = FMT == LSSM_W_Q4_G64 || FMT == LSSM_W_Q4_B32;
+    const uint32_t tiles = (N + 15) / 16, cus = num_cus();
+    uint32_t want = (tiles + cus - 1) / cus;             // tiles per block: blocks ~ CUs
+    want = want < 1 ? 1 : (want > 4 ? 4 : want);
+    // the most tiles (up to want), then the fewest quads per wave, such that
+    // the shape is built and its waves split K into whole quads
+    for (uint32_t ct = want; ct >= 1 && p.qpw == 0; --ct) {
+        for (uint32_t q : {1u, 2u, 4u, 8u}) {
+            // every output element has a thread: 64 KS ((ct + 1) / 2) >= 256 ct
+            if (mma_shape_ok((int)ct, (int)q, q4) && quads % q == 0 && (quads / q) * ((ct + 1) / 2) >= 4 * ct &&
+                quads / q <= (uint32_t)mma_waves((int)ct, (int)q)) {
+                p.qpw = q;
+                p.ct = ct;
+                break;
+            }
+        }
+    }
+    if (p.qpw == 0) return false;
+    p.ks = quads / p.qpw;
+    // a wave's scales are loaded as one vector: their offset in a row must be
+    // a multiple of their count (P::GPQ * qpw half-words, at least 2)
+    const uint32_t nsc = std::max<uint32_t>(P::GPQ * p.qpw, 2u);
+    if (P::G > 0 && (K / P::G) % nsc != 0) return false;
+    const size_t RS = K / 2 + 4, seg = (K / 8 + 63) / 64;
+    size_t fit = MM_LDS_MAX / (RS * 4);
+    fit = fit < 16 ? fit : 16;
+    fit = fit < MM_MAXJ * p.ks / seg ? fit : MM_MAXJ * p.ks / seg;   // staged segments per wave
+    if (fit < 1) return false;
+    const uint32_t passes = (uint32_t)((M + fit - 1) / fit);
+    p.mpb = (M + passes - 1) / passes;
+    const size_t ra = std::max((size_t)p.mpb * RS, (size_t)p.ks * p.ct * WAVE * 4);
+    p.ra = (uint32_t)ra;
+    p.lds = ra * 4;
+    return p.lds <= MM_LDS_MAX;
+}
+
+template <typename T> bool mma_aligned(const GemvCore& c, bool norm) {
+    return (uintptr_t)c.x % 16 == 0 && ((size_t)c.x_stride * sizeof(T)) % 16 == 0 &&
+           (!norm || (uintptr_t)c.norm_w % 16 == 0) && (uintptr_t)c.w % 16 == 0 && (uintptr_t)c.s % 16 == 0;
+}
+
+template <int FMT, typename T, int CT, int QPW, bool NORM, class Epi>
+hipError_t mma_run(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmaPlan& p) {
+    auto k = gemv_mma_kernel<FMT, T, CT, QPW, NORM, Epi>;
+    // opt in to the dynamic LDS once per instantiation (a host attribute)
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)MM_LDS_MAX);
+    if (attr != hipSuccess) return attr;
+    const uint32_t tiles = (c.N + 15) / 16;
+    k<<<(tiles + CT - 1) / CT, WAVE * p.ks, p.lds, s>>>(c, e, M, p.mpb, p.ra);
+    return hipGetLastError();
+}
+
+template <int FMT, typename T, bool NORM, class Epi>
+hipError_t mma_shape(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmaPlan& p) {
+    if (p.ct == 1) {
+        switch (p.qpw) {
+            case 1: return mma_run<FMT, T, 1, 1, NORM, Epi>(s, c, e, M, p);
+            case 2: return mma_run<FMT, T, 1, 2, NORM, Epi>(s, c, e, M, p);
+            case 4: return mma_run<FMT, T, 1, 4, NORM, Epi>(s, c, e, M, p);
+            default: return mma_run<FMT, T, 1, 8, NORM, Epi>(s, c, e, M, p);
+        }
+    }
+    if constexpr (FMT == LSSM_W_Q4_G64 || FMT == LSSM_W_Q4_B32) {
+        if (p.qpw == 4) return mma_run<FMT, T, 4, 4, NORM, Epi>(s, c, e, M, p);
+        switch (p.ct) {
+            case 2: return mma_run<FMT, T, 2, 2, NORM, Epi>(s, c, e, M, p);
+            case 3: return mma_run<FMT, T, 3, 2, NORM, Epi>(s, c, e, M, p);
+            default: return mma_run<FMT, T, 4, 2, NORM, Epi>(s, c, e, M, p);
+        }
+    }
+    return hipErrorInvalidValue;                       // not a planned shape
+}
+
+// Formats the MFMA decode kernel takes: int4 (both layouts) with fp16 / bf16,
+// int8 and dense weights with fp16.
+template <typename T, class F> bool mma_fmt(int wfmt, F&& f) {
+    if constexpr (__is_same(T, float)) {
+        return false;
+    } else {
+        switch (wfmt) {
+            case LSSM_W_Q4_G64: return f(FmtTag<LSSM_W_Q4_G64>{});
+            case LSSM_W_Q4_B32: return f(FmtTag<LSSM_W_Q4_B32>{});
+            case LSSM_W_Q8_G32:
+                if constexpr (__is_same(T, f16)) return f(FmtTag<LSSM_W_Q8_G32>{});
+                else return false;
+            case LSSM_W_DENSE:
+                if constexpr (__is_same(T, f16)) return f(FmtTag<LSSM_W_DENSE>{});
+                else return false;
+            default: return false;
+        }
+    }
+}
+
+// Runs the MFMA decode kernel when it takes this call (returns false, and
+// launches nothing, otherwise).
+// Only RMSNorm-fused calls (the engine's decode linears and inproj_decode).
+template <typename T, class Epi>
+bool try_mma(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, int wfmt, bool norm, hipError_t& err) {
+    if (!norm || !mma_aligned<T>(c, norm)) return false;
+    return mma_fmt<T>(wfmt, [&](auto tag) -> bool {
+        constexpr int FMT = decltype(tag)::value;
+        MmaPlan p;
+        if (!mma_plan<FMT, T>(M, c.N, c.K, p)) return false;
+        err = mma_shape<FMT, T, true, Epi>(s, c, e, M, p);
+        return true;
+    });
+}
+
+template <typename T> bool mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt) {
+    return mma_fmt<T>(wfmt, [&](auto tag) -> bool {
+        MmaPlan p;
+        return mma_plan<decltype(tag)::value, T>(M, N, K, p);
+    });
+}
+
+}  // namespace
+
+bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
+    if (act == LSSM_F16) return mma_takes<f16>(M, N, K, wfmt);
+    if (act == LSSM_BF16) return mma_takes<bf16>(M, N, K, wfmt);
+    return false;
+}
+
+bool launch_gemv_mma(hipStream_t s, const GemvArgs& a, hipError_t& err) {
+    if (a.M < 2) return false;
+    GemvCore c{a.x, a.x_stride, (const uint8_t*)a.w, (const uint16_t*)a.s, a.norm_w, a.eps, a.N, a.K, 1.0f / (float)a.K};
+    auto go = [&](auto tag) -> bool {
+        using T = decltype(tag);
+        EpiPlain<T> e{(T*)a.y, a.y_stride, (const T*)a.res, a.epi};
+        return try_mma<T>(s, c, e, a.M, a.wfmt, a.norm_w != nullptr, err);
+    };
+    if (a.act == LSSM_F16) return go(f16{});
+    if (a.act == LSSM_BF16) return go(bf16{});
+    return false;
+}
+
+bool launch_inproj_decode_mma(hipStream_t s, const InprojDecodeArgs& a, hipError_t& err) {
+    const GemvArgs& g = a.g;
+    if (g.M < 2) return false;
+    GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
+    auto go = [&](auto tag) -> bool {
+        using T = decltype(tag);
+        EpiInproj<T> e{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,
+                       (const T*)a.conv_b, (T*)a.z, (T*)a.xbc_act, (T*)a.dt};
+        return try_mma<T>(s, c, e, g.M, g.wfmt, g.norm_w != nullptr, err);
+    };
+    if (g.act == LSSM_F16) return go(f16{});
+    if (g.act == LSSM_BF16) return go(bf16{});
+    return false;
+}
+
+}  // namespace lssm

@@ -110,6 +110,7 @@ hipError_t launch_gemv(hipStream_t s, const GemvArgs& a);
 // 16-byte aligned operands / with any alignment.
 int gemv_max_rows(uint32_t K, int wfmt, int act);
 int gemv_lds_rows(uint32_t K, int wfmt, int act);
+
 hipError_t launch_dequant(hipStream_t s, const void* w, const void* sc, float* out, uint32_t N,
                           uint32_t K, int wfmt);
 
@@ -169,5 +170,14 @@ struct InprojDecodeArgs {
     void* dt;             // [B, H]
 };
 hipError_t launch_inproj_decode(hipStream_t s, const InprojDecodeArgs& a);
+
+// MFMA GEMV for decode batches (gemv_mma.hip): 2..64 rows, GEMV rule, RMSNorm
+// prologue when norm_w is set.  Returns false (launching nothing) when the
+// shape, format or alignment is not one it takes; err holds the launch result.
+bool launch_gemv_mma(hipStream_t s, const GemvArgs& a, hipError_t& err);
+bool launch_inproj_decode_mma(hipStream_t s, const InprojDecodeArgs& a, hipError_t& err);
+// Whether a decode batch of M rows runs in one MFMA launch (16-byte aligned
+// operands assumed; otherwise the launchers fall back to gemv1 launches).
+bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);
 
 }  // namespace lssm

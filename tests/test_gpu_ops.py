@@ -398,12 +398,27 @@ def test_inproj_fused_vs_oracle(ctx, rng):
         assert_close(act_host(o, O.F16), r, O.F16, 2e-3, "inproj_fused")
 
 
-@pytest.mark.parametrize("act,wfmt,batch", [(O.BF16, O.W_Q4_G64, 1), (O.F16, O.W_Q8_G32, 3),
-                                            (O.F16, O.W_Q4_B32, 4), (O.F32, O.W_DENSE, 2)])
-def test_inproj_decode_vs_unfused_chain(ctx, rng, act, wfmt, batch):
-    """The engine's fused decode in_proj == rmsnorm -> gemv -> conv update -> split SiLU."""
+INPROJ_CASES = [
+    # batch 1..4: VALU GEMV (gemv1 / gemv_lds)
+    (O.BF16, O.W_Q4_G64, 1, 2560), (O.F16, O.W_Q8_G32, 3, 2560), (O.F16, O.W_Q4_B32, 4, 2560),
+    (O.F32, O.W_DENSE, 2, 2560),
+    # 2..64: MFMA GEMV (2.7B in_proj: 3 tiles per block); 17 and 33 end
+    # mid-tile, 64 fills four MFMA row tiles in four passes of 16 rows
+    (O.BF16, O.W_Q4_G64, 2, 2560), (O.BF16, O.W_Q4_G64, 16, 2560), (O.BF16, O.W_Q4_G64, 17, 2560),
+    (O.BF16, O.W_Q4_G64, 64, 2560), (O.F16, O.W_Q4_G64, 8, 2560), (O.BF16, O.W_Q4_B32, 5, 2560),
+    (O.F16, O.W_Q4_B32, 33, 2560), (O.F16, O.W_Q8_G32, 16, 2560), (O.F16, O.W_DENSE, 7, 2560),
+    # K = 5120: 16 rows take two passes of 8 (staging does not fit 16)
+    (O.BF16, O.W_Q4_G64, 16, 5120), (O.F16, O.W_Q8_G32, 12, 5120),
+]
+
+
+@pytest.mark.parametrize("act,wfmt,batch,d_model", INPROJ_CASES,
+                         ids=[f"{['f16', 'bf16', 'f32'][a]}-w{w}-b{b}-k{k}" for a, w, b, k in INPROJ_CASES])
+def test_inproj_decode_vs_unfused_chain(ctx, rng, act, wfmt, batch, d_model):
+    """The engine's fused decode in_proj == rmsnorm -> gemv -> conv update -> split
+    SiLU, with the GEMV rule (exact dequantization) at every batch."""
     L = _lib()
-    d_model, d_inner, N, G, H, K = 2560, 5120, 128, 1, 80, 4
+    d_inner, N, G, H, K = (5120, 128, 1, 80, 4) if d_model == 2560 else (1024, 64, 2, 16, 4)
     xbc = d_inner + 2 * G * N
     proj = d_inner + xbc + H
     hid = O.to_act(rng.standard_normal((batch, d_model)) * 0.5, act)
@@ -428,6 +443,77 @@ def test_inproj_decode_vs_unfused_chain(ctx, rng, act, wfmt, batch):
     ref = O.silu(conv, act)
     assert_close(act_host(xa, act), ref, act, bound * 4, "xbc_act")
     assert_close(act_host(csd, act), cs2, act, bound, "conv_state")
+
+
+NORM_LINEAR_CASES = [
+    # rows, N, K, act, wfmt, epi: 2.7B out_proj (K 5120: 16 rows in two passes),
+    # 8B out_proj (K 8192), odd N, the VALU GEMV rows (1, 3) and the fallback
+    # formats (bf16 dense / int8 take gemv1 launches of <= 4 rows)
+    (16, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD), (4, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD),
+    (40, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD), (64, 1000, 2560, O.F16, O.W_Q4_B32, O.EPI_NONE),
+    (9, 4096, 8192, O.BF16, O.W_Q4_G64, O.EPI_ADD), (2, 300, 1024, O.F16, O.W_Q8_G32, O.EPI_SILU),
+    (24, 520, 1536, O.F16, O.W_DENSE, O.EPI_ADD), (1, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD),
+    (3, 777, 2560, O.BF16, O.W_Q4_B32, O.EPI_NONE), (6, 512, 1024, O.BF16, O.W_DENSE, O.EPI_NONE),
+]
+
+
+@pytest.mark.parametrize("rows,N,K,act,wfmt,epi", NORM_LINEAR_CASES,
+                         ids=[f"m{m}-n{n}-k{k}-{['f16', 'bf16', 'f32'][a]}-w{w}-e{e}" for m, n, k, a, w, e in NORM_LINEAR_CASES])
+def test_norm_linear_decode_vs_oracle(ctx, rng, rows, N, K, act, wfmt, epi):
+    """RMSNorm + linear (+ residual) for decode rows: the GEMV rule (exact
+    dequantization) at every row count, against the oracle's chain."""
+    L = _lib()
+    x = O.to_act(rng.standard_normal((rows, K)) * 0.7, act)
+    nw = O.to_act(1 + 0.1 * rng.standard_normal(K), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    res = O.to_act(rng.standard_normal((rows, N)), act)
+    y = dev(res) if epi == O.EPI_ADD else empty((rows, N), act)
+    L.check(L.lib.lssm_norm_linear_decode(ctx.h, dev(x).data_ptr(), dev(nw).data_ptr(), 1e-5,
+                                          dev(w).data_ptr(), None if s is None else dev(s).data_ptr(),
+                                          y.data_ptr(), y.data_ptr() if epi == O.EPI_ADD else None,
+                                          rows, N, K, wfmt, act, epi))
+    normed = O.rmsnorm(x, nw, 1e-5, act)
+    ref = O.linear(normed, w, s, rows, N, K, wfmt, act, epi=epi, residual=res if epi == O.EPI_ADD else None)
+    assert_close(act_host(y, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2}[act], "norm_linear_decode")
+
+
+def test_norm_linear_decode_graph_replays_match_eager(ctx, rng):
+    """The MFMA decode GEMV (16 rows, 2.7B out_proj) replayed from a HIP graph
+    gives the eager bits on every replay (no memset nodes, deterministic sums)."""
+    L = _lib()
+    rows, N, K = 16, 2560, 5120
+    x = dev(O.to_act(rng.standard_normal((rows, K)) * 0.7, O.BF16))
+    nw = dev(O.to_act(1 + 0.1 * rng.standard_normal(K), O.BF16))
+    w, s = _weights(rng, N, K, O.W_Q4_G64, O.BF16)
+    wd, sd = dev(w), dev(s)
+    y = empty((rows, N), O.BF16)
+    run = lambda: L.check(L.lib.lssm_norm_linear_decode(ctx.h, x.data_ptr(), nw.data_ptr(), 1e-5, wd.data_ptr(),
+                                                        sd.data_ptr(), y.data_ptr(), None, rows, N, K,
+                                                        O.W_Q4_G64, O.BF16, O.EPI_NONE))
+    run()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    c2 = L.Ctx(st.cuda_stream)
+    y.zero_()
+    torch.cuda.synchronize()
+    c2.begin_batch()                      # enqueue only: no stream sync inside the capture
+    with torch.cuda.stream(st):
+        g.capture_begin()
+        L.check(L.lib.lssm_norm_linear_decode(c2.h, x.data_ptr(), nw.data_ptr(), 1e-5, wd.data_ptr(),
+                                              sd.data_ptr(), y.data_ptr(), None, rows, N, K,
+                                              O.W_Q4_G64, O.BF16, O.EPI_NONE))
+        g.capture_end()
+    c2.commit_and_wait()
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        run()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
 
 
 @pytest.mark.parametrize("act", [O.F16, O.BF16])
