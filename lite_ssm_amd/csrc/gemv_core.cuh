@@ -185,11 +185,13 @@ template <typename T> struct EpiInproj {
             bool done = false;
             if constexpr (kVec) {
                 if (dconv == 4) {
-                    const T* s = reinterpret_cast<const T*>(&p.s);
-                    const T* w = reinterpret_cast<const T*>(&p.w);
+                    // taps and weights by bit extraction (an address of the
+                    // registers would put them in scratch)
+                    auto lo = [](uint32_t d) { return f_of_raw<T>(d & 0xFFFFu); };
+                    auto hi = [](uint32_t d) { return f_of_raw<T>(d >> 16); };
                     // window shift (conv1d.metal:127-130): taps 1..3 move down, x lands in 3
-                    a = f_of_raw<T>(p.b) + to_f(s[1]) * to_f(w[0]) + to_f(s[2]) * to_f(w[1]) +
-                        to_f(s[3]) * to_f(w[2]) + to_f(v) * to_f(w[3]);
+                    a = f_of_raw<T>(p.b) + hi(p.s.x) * lo(p.w.x) + lo(p.s.y) * hi(p.w.x) +
+                        hi(p.s.y) * lo(p.w.y) + to_f(v) * hi(p.w.y);
                     uint2 ns;
                     ns.x = p.s.x >> 16 | p.s.y << 16;                                     // (s1, s2)
                     ns.y = p.s.y >> 16 | (uint32_t)__builtin_bit_cast(uint16_t, v) << 16;  // (s3, x)

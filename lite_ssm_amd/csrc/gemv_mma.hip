@@ -375,15 +375,16 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
             m = base + 4 * (l / 16) + e;
             n = 16 * (tile0 + t) + l % 16;
         };
+        // unconditional (clamped) and pinned ahead of the compute: a branch
+        // around them, or their sinking to the epilogue, would expose their latency
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
-            const uint32_t o = threadIdx.x + NT * k;
-            if (o < CT * 256u) {
-                uint32_t m, n;
-                out_mn(o, m, n);
-                pre[k] = epi.prefetch((int)min(m, M - 1), min(n, N - 1));
-            }
+            uint32_t m, n;
+            out_mn(min(threadIdx.x + NT * k, CT * 256u - 1), m, n);
+            pre[k] = epi.prefetch((int)min(m, M - 1), min(n, N - 1));
         }
+        __builtin_amdgcn_sched_barrier(0);
         floatx4 acc[CT];
 #pragma unroll
         for (int t = 0; t < CT; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
