@@ -197,32 +197,31 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
             if constexpr (NORM) nv = reinterpret_cast<const u32x4*>(c.norm_w)[cc];
         };
         if constexpr (NORM) {
-            // sum(x^2) per segment, then 1 / rms per row (segments in order)
-            u32x4 xv[MM_MAXJ];
-#pragma unroll
-            for (int j = 0; j < MM_MAXJ; ++j) {
-                if (w + KS * j < nseg) {
-                    if constexpr (KEEP) {
-                        xv[j] = xk[j];
-                    } else {
-                        u32x4 dummy;
-                        load(j, xv[j], dummy);
-                    }
-                }
-            }
-            // each lane's share in LDS (region A, before x lands there), then
-            // one wave per row sums it in a fixed order
+            // sum(x^2) per segment: each lane's share in LDS (region A, before
+            // x lands there), then one wave per row sums it in a fixed order
             float* part = reinterpret_cast<float*>(mm_lds);    // [segment][lane]
-#pragma unroll
-            for (int j = 0; j < MM_MAXJ; ++j) {
+            auto squares = [&](int j, const u32x4& d) {
                 const uint32_t u = w + KS * j;
-                if (u < nseg) {
-                    const u32x4 d = xv[j];
-                    float q = dot2(d[0], d[0], 0.0f, T{});
-                    q = dot2(d[1], d[1], q, T{});
-                    q = dot2(d[2], d[2], q, T{});
-                    q = dot2(d[3], d[3], q, T{});
-                    part[u * WAVE + lane] = (u % SEG) * 64 + lane < KO ? q : 0.0f;
+                float q = dot2(d[0], d[0], 0.0f, T{});
+                q = dot2(d[1], d[1], q, T{});
+                q = dot2(d[2], d[2], q, T{});
+                q = dot2(d[3], d[3], q, T{});
+                part[u * WAVE + lane] = (u % SEG) * 64 + lane < KO ? q : 0.0f;
+            };
+            if constexpr (KEEP) {
+#pragma unroll
+                for (int j = 0; j < MM_MAXJ; ++j)
+                    if (w + KS * j < nseg) squares(j, xk[j]);
+            } else {
+                // rounds of MM_MAXJ / 2 segments (any number of them per wave)
+                for (int j0 = 0; w + KS * j0 < nseg; j0 += MM_MAXJ / 2) {
+                    u32x4 xv[MM_MAXJ / 2], dummy;
+#pragma unroll
+                    for (int jj = 0; jj < MM_MAXJ / 2; ++jj)
+                        if (w + KS * (j0 + jj) < nseg) load(j0 + jj, xv[jj], dummy);
+#pragma unroll
+                    for (int jj = 0; jj < MM_MAXJ / 2; ++jj)
+                        if (w + KS * (j0 + jj) < nseg) squares(j0 + jj, xv[jj]);
                 }
             }
             lds_barrier();
@@ -262,30 +261,35 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
             // the pairs of k .. k + 7 sit at dwords k / 2 .. k / 2 + 3 of the row
             if (live) *reinterpret_cast<u32x4*>(xl + r * RS + 4 * cc) = pk;
         };
-        // the rows' 1 / rms first, all at once (one LDS wait, not one per segment)
-        float rr[MM_MAXJ];
-#pragma unroll
-        for (int j = 0; j < MM_MAXJ; ++j) {
-            rr[j] = 1.0f;
-            if constexpr (NORM) {
-                if (w + KS * j < nseg) rr[j] = rinv_s[(w + KS * j) / SEG];
-            }
-        }
         if constexpr (KEEP) {
+            // the rows' 1 / rms first, all at once (one LDS wait, not one per segment)
+            float rr[MM_MAXJ];
+#pragma unroll
+            for (int j = 0; j < MM_MAXJ; ++j) {
+                rr[j] = 1.0f;
+                if constexpr (NORM) {
+                    if (w + KS * j < nseg) rr[j] = rinv_s[(w + KS * j) / SEG];
+                }
+            }
 #pragma unroll
             for (int j = 0; j < MM_MAXJ; ++j)
                 if (w + KS * j < nseg) put(j, xk[j], nk[j], rr[j]);
         } else {
-            // half of the segments at a time
-#pragma unroll
-            for (int h = 0; h < MM_MAXJ; h += MM_MAXJ / 2) {
+            // rounds of MM_MAXJ / 2 segments (any number of them per wave)
+            for (int j0 = 0; w + KS * j0 < nseg; j0 += MM_MAXJ / 2) {
                 u32x4 xv[MM_MAXJ / 2], nv[MM_MAXJ / 2];
+                float rr[MM_MAXJ / 2];
+#pragma unroll
+                for (int jj = 0; jj < MM_MAXJ / 2; ++jj) {
+                    rr[jj] = 1.0f;
+                    if (w + KS * (j0 + jj) < nseg) {
+                        load(j0 + jj, xv[jj], nv[jj]);
+                        if constexpr (NORM) rr[jj] = rinv_s[(w + KS * (j0 + jj)) / SEG];
+                    }
+                }
 #pragma unroll
                 for (int jj = 0; jj < MM_MAXJ / 2; ++jj)
-                    if (w + KS * (h + jj) < nseg) load(h + jj, xv[jj], nv[jj]);
-#pragma unroll
-                for (int jj = 0; jj < MM_MAXJ / 2; ++jj)
-                    if (w + KS * (h + jj) < nseg) put(h + jj, xv[jj], nv[jj], rr[h + jj]);
+                    if (w + KS * (j0 + jj) < nseg) put(j0 + jj, xv[jj], nv[jj], rr[jj]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -293,10 +297,10 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
     };
 
     // ---- weights (and raw scale bits) of the wave's quads, all in flight ----
-    // With few weight registers (CT * QPW <= 4) they are held over all
+    // With few weight registers (CT * QPW <= 8) they are held over all
     // passes; otherwise a later pass reads them again (L2 hits) rather than
     // holding them across its staging.
-    constexpr bool HOLD = CT * QPW <= 4;
+    constexpr bool HOLD = CT * QPW <= 8;
     const size_t rb = F::row_bytes(K);
     u32x4 wr[CT][QPW];
     constexpr int SW = (QPW * GPQ + 1) / 2;                    // scale dwords per tile and wave
@@ -335,7 +339,8 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
     // x of the first pass, staged before any weight is requested: requested
     // behind the weights, x would queue behind the whole chip's weight
     // traffic (measured: staging done ~7 us after the start instead of ~2)
-    {
+    const bool keep0 = mpb * SEG <= (uint32_t)(MM_MAXJ * KS);   // the first pass's x fits the registers
+    if (keep0) {
         const uint32_t nseg = mpb * SEG;
         const uint32_t lane0 = threadIdx.x % WAVE;
         // KS a multiple of SEG: every segment of a wave sits at the same place
@@ -354,7 +359,8 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
             }
         }
     }
-    stage(0u, FmtTag<1>{});
+    if (keep0) stage(0u, FmtTag<1>{});
+    else stage(0u, FmtTag<0>{});
     load_w();
 
     for (uint32_t base = 0; base < M; base += mpb) {
@@ -499,10 +505,9 @@ template <int FMT, typename T> bool mma_plan(uint32_t M, uint32_t N, uint32_t K,
     // a multiple of their count (P::GPQ * qpw half-words, at least 2)
     const uint32_t nsc = std::max<uint32_t>(P::GPQ * p.qpw, 2u);
     if (P::G > 0 && (K / P::G) % nsc != 0) return false;
-    const size_t RS = K / 2 + 4, seg = (K / 8 + 63) / 64;
+    const size_t RS = K / 2 + 4;
     size_t fit = MM_LDS_MAX / (RS * 4);
     fit = fit < 16 ? fit : 16;
-    fit = fit < MM_MAXJ * p.ks / seg ? fit : MM_MAXJ * p.ks / seg;   // staged segments per wave
     if (fit < 1) return false;
     const uint32_t passes = (uint32_t)((M + fit - 1) / fit);
     p.mpb = (M + passes - 1) / passes;

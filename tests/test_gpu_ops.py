@@ -409,6 +409,8 @@ INPROJ_CASES = [
     (O.F16, O.W_Q4_B32, 33, 2560), (O.F16, O.W_Q8_G32, 16, 2560), (O.F16, O.W_DENSE, 7, 2560),
     # K = 5120: 16 rows take two passes of 8 (staging does not fit 16)
     (O.BF16, O.W_Q4_G64, 16, 5120), (O.F16, O.W_Q8_G32, 12, 5120),
+    # 8B in_proj shape at batch 32 (4 tiles per block, 2 passes)
+    (O.BF16, O.W_Q4_G64, 32, 4096),
 ]
 
 
@@ -418,7 +420,8 @@ def test_inproj_decode_vs_unfused_chain(ctx, rng, act, wfmt, batch, d_model):
     """The engine's fused decode in_proj == rmsnorm -> gemv -> conv update -> split
     SiLU, with the GEMV rule (exact dequantization) at every batch."""
     L = _lib()
-    d_inner, N, G, H, K = (5120, 128, 1, 80, 4) if d_model == 2560 else (1024, 64, 2, 16, 4)
+    d_inner, N, G, H, K = {2560: (5120, 128, 1, 80, 4), 5120: (1024, 64, 2, 16, 4),
+                           4096: (8192, 128, 8, 128, 4)}[d_model]
     xbc = d_inner + 2 * G * N
     proj = d_inner + xbc + H
     hid = O.to_act(rng.standard_normal((batch, d_model)) * 0.5, act)
@@ -451,7 +454,8 @@ NORM_LINEAR_CASES = [
     # formats (bf16 dense / int8 take gemv1 launches of <= 4 rows)
     (16, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD), (4, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD),
     (40, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD), (64, 1000, 2560, O.F16, O.W_Q4_B32, O.EPI_NONE),
-    (9, 4096, 8192, O.BF16, O.W_Q4_G64, O.EPI_ADD), (2, 300, 1024, O.F16, O.W_Q8_G32, O.EPI_SILU),
+    (9, 4096, 8192, O.BF16, O.W_Q4_G64, O.EPI_ADD), (32, 4096, 8192, O.BF16, O.W_Q4_G64, O.EPI_ADD),
+    (2, 300, 1024, O.F16, O.W_Q8_G32, O.EPI_SILU),
     (24, 520, 1536, O.F16, O.W_DENSE, O.EPI_ADD), (1, 2560, 5120, O.BF16, O.W_Q4_G64, O.EPI_ADD),
     (3, 777, 2560, O.BF16, O.W_Q4_B32, O.EPI_NONE), (6, 512, 1024, O.BF16, O.W_DENSE, O.EPI_NONE),
 ]
