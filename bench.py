@@ -7,9 +7,10 @@ d_state 128, 1 group, conv 4, vocab 50280, random-init weights resident in HBM.
                 64 layers + lm_head + argmax, replayed as one HIP graph);
   * prefill   = 4 x 4096 token prefill, tokens/s and MFMA utilisation;
   * decode at batch 4 / 16 is reported alongside;
-  * roofline  = the dominant decode kernel (fused RMSNorm + in_proj GEMV + conv
-                update), algorithmic bytes per launch / its average launch time
-                measured here with HIP events on the library's stream;
+  * roofline  = the dominant decode kernel (RMSNorm + in_proj GEMV + conv update
+                + SSD step in one launch), algorithmic bytes per launch / its
+                average launch time measured here with HIP events on the
+                library's stream;
   * cpu_baseline = the CPU oracle (a C restatement of the reference kernels; the
                 reference itself has no CPU path) on a bounded sample.
 
@@ -33,23 +34,52 @@ def ssd_flops_per_token_head(Q=64, N=128, P=64):
     return 2 * Q * N + 2 * Q * P + 4 * N * P
 
 
-def inproj_args(L, m, sh, Lw, bufs):
-    """Arguments of one lssm_inproj_decode launch (batch 1) on layer weights Lw."""
-    hid, cst, zb, xb, db = bufs
-    return (hid.data_ptr(), Lw["norm_w"].data_ptr(), Lw["in_proj_w"].data_ptr(),
-            Lw["in_proj_s"].data_ptr(), cst.data_ptr(), Lw["conv1d_w"].data_ptr(),
-            Lw["conv1d_b"].data_ptr(), zb.data_ptr(), xb.data_ptr(), db.data_ptr(), 1,
-            sh.d_model, sh.d_inner, sh.d_state, sh.n_groups, sh.n_heads, sh.d_conv, 1e-5,
-            L.W_Q4_G64, L.BF16)
-
-
-def inproj_buffers(sh):
+def fused_buffers(sh):
+    """Per-launch buffers of the dominant decode kernel (batch 1): hidden, conv
+    state, SSD state, gated SSD output, the projection's tagged words."""
     import torch
     return (torch.randn(1, sh.d_model, device="cuda").to(torch.bfloat16),
             torch.zeros(sh.xbc, sh.d_conv, dtype=torch.bfloat16, device="cuda"),
+            torch.zeros(sh.n_heads, sh.d_head, sh.d_state, dtype=torch.float32, device="cuda"),
             torch.empty(sh.d_inner, dtype=torch.bfloat16, device="cuda"),
-            torch.empty(sh.xbc, dtype=torch.bfloat16, device="cuda"),
-            torch.empty(sh.n_heads, dtype=torch.bfloat16, device="cuda"))
+            torch.zeros(sh.proj, dtype=torch.int64, device="cuda"))
+
+
+def fused_launcher(L, ctx, m, sh, bufs):
+    """All layers' lssm_inproj_ssd_decode launches (the engine's batch-1 decode
+    kernel: RMSNorm + in_proj GEMV + conv update + SiLU + SSD step + SiLU(z)
+    gate), one per layer; every call takes a new tag."""
+    hid, cst, sst, y, xfer = bufs
+    fn = L.lib.lssm_inproj_ssd_decode
+    pre = [(hid.data_ptr(), Lw["norm_w"].data_ptr(), Lw["in_proj_w"].data_ptr(), Lw["in_proj_s"].data_ptr(),
+            cst.data_ptr(), Lw["conv1d_w"].data_ptr(), Lw["conv1d_b"].data_ptr(), Lw["dt_bias"].data_ptr(),
+            Lw["A_log"].data_ptr(), Lw["D"].data_ptr(), sst.data_ptr(), y.data_ptr(), xfer.data_ptr())
+           for Lw in m.layers]
+    post = (sh.d_model, sh.d_inner, sh.d_state, sh.n_groups, sh.n_heads, sh.d_head, sh.d_conv, 1e-5,
+            L.W_Q4_G64, L.BF16)
+    tag = [0]
+
+    def run():
+        bad = 0
+        for a in pre:
+            tag[0] += 1
+            bad |= fn(ctx.h, *a, tag[0], *post)
+        L.check(bad)
+    return run
+
+
+def fused_bytes(m, sh):
+    """Algorithmic bytes of one launch: int4 weights + fp16 scales, hidden and
+    norm weight, conv state read + write, conv weight + bias, SSD state read +
+    write, A_log / dt_bias / D, the gated output (the tagged words that carry
+    the projection between workgroups are not counted)."""
+    Lw0 = m.layers[0]
+    return (Lw0["in_proj_w"].numel() + Lw0["in_proj_s"].numel() * 2 +
+            (sh.d_model * 2) * 2 +
+            sh.xbc * sh.d_conv * 2 * 2 + sh.xbc * (sh.d_conv + 1) * 2 +
+            2 * sh.n_heads * sh.d_head * sh.d_state * 4 +
+            3 * sh.n_heads * 2 +
+            sh.d_inner * 2)
 
 
 def profile_kernel(L, ctx, m, sh, stream):
@@ -57,19 +87,17 @@ def profile_kernel(L, ctx, m, sh, stream):
     64 layers' weights, 10 times, then a 256 MiB device-to-device copy 10 times
     (the known-size reference that scales the FETCH_SIZE / WRITE_SIZE counters)."""
     import torch
-    bufs = inproj_buffers(sh)
-    args = [inproj_args(L, m, sh, Lw, bufs) for Lw in m.layers]
+    run = fused_launcher(L, ctx, m, sh, fused_buffers(sh))
     ctx.begin_batch()
     for _ in range(10):
-        for a in args:
-            L.check(L.lib.lssm_inproj_decode(ctx.h, *a))
+        run()
     ctx.commit_and_wait()
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"profile_kernel": "inproj_decode", "launches": 10 * len(args),
+    print(json.dumps({"profile_kernel": "inproj_ssd_decode", "launches": 10 * sh.n_layer,
                       "copy_bytes": src.numel(), "copies": 10}), flush=True)
 
 
@@ -174,29 +202,16 @@ def main():
         print(f"[bench] decode bs={b}: {tbt / n * 1e3:.3f} ms/step", file=sys.stderr, flush=True)
 
     # ---------------- dominant kernel, live (HIP events on the library's stream) ----------------
-    bufs = inproj_buffers(sh)
-    kargs = [inproj_args(L, m, sh, Lw, bufs) for Lw in m.layers]
-    fn = L.lib.lssm_inproj_decode
-
-    def inproj_all_layers():
-        bad = 0
-        for a in kargs:
-            bad |= fn(ctx.h, *a)
-        L.check(bad)
-
+    run = fused_launcher(L, ctx, m, sh, fused_buffers(sh))
     ctx.begin_batch()
-    inproj_all_layers()
+    run()
     reps = 10
-    t_k = timed(inproj_all_layers, reps)
+    t_k = timed(run, reps)
     ctx.commit_and_wait()
     k_us = t_k / (reps * sh.n_layer) * 1e6
-    Lw0 = m.layers[0]
-    k_bytes = (Lw0["in_proj_w"].numel() + Lw0["in_proj_s"].numel() * 2 +      # weights
-               (sh.d_model * 2) * 2 +                                          # hidden + norm_w
-               sh.xbc * sh.d_conv * 2 * 2 + sh.xbc * (sh.d_conv + 1) * 2 +     # conv state r/w + w, b
-               sh.proj * 2)                                                    # z | xbc_act | dt out
+    k_bytes = fused_bytes(m, sh)
     achieved = k_bytes / (k_us * 1e-6) / 1e9
-    print(f"[bench] inproj_decode: {k_us:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+    print(f"[bench] inproj_ssd_decode: {k_us:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
     # ---------------- CPU baseline (oracle, bounded sample) ----------------
     cpu = None
@@ -225,7 +240,7 @@ def main():
     # HBM bytes per launch of the same kernel from the two rocprofv3 --pmc passes
     # (FETCH_SIZE, WRITE_SIZE, calibrated on a 256 MiB copy), recorded in profiles/
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "inproj_decode_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "inproj_ssd_decode_traffic.json")
     if args.model == "mamba2-2.7b" and os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("traffic_bytes")
 
@@ -248,7 +263,8 @@ def main():
                    "batch": 1, "prefill": f"{PB}x{PL}"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "inproj_decode (RMSNorm + in_proj int4-g64 GEMV + conv update + SiLU)",
+                     "kernel": "inproj_ssd_decode (RMSNorm + in_proj int4-g64 GEMV + conv update + SiLU "
+                               "+ SSD step + SiLU(z) gate, one launch per layer)",
                      "bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_us, 3)},
         "cpu_baseline": cpu,
         "step_hbm_frac": round((wbytes + 2 * state_bytes) / (t_dec / args.steps) / 1e9 / HBM_PEAK_GBS, 4),

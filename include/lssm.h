@@ -280,6 +280,27 @@ int lssm_inproj_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, co
                        uint32_t n_heads, uint32_t d_conv, float eps, lssm_wfmt wfmt,
                        lssm_dtype act);
 
+/* Batch-1 decode of one layer's mixer input in ONE launch: lssm_inproj_decode
+ * (batch 1) followed by the SSD step (lssm_ssd_step, ssd_step.metal:33-77) and
+ * the SiLU(z) gate, y = r(silu(z) * r(C.S' + D x)).  The projection rows travel
+ * between the launch's workgroups as 64-bit words (value | tag << 32) in
+ * `xfer` ([d_inner + xBC_dim + n_heads] words, zeroed before its first use);
+ * `tag` must differ from the tag of the previous call on the same `xfer`
+ * (e.g. a step counter from 1).  ssd_state [n_heads, d_head, d_state] fp32 is
+ * updated in place, conv_state as in lssm_inproj_decode; y [d_inner].
+ * Takes d_state 128, d_head a multiple of 32, d_conv 4, fp16 / bf16, int4-g64
+ * (or int8-g32 with fp16) weights, and grids of at most one workgroup per CU;
+ * other shapes return LSSM_EINVAL (nothing runs).  No counterpart in the
+ * reference, whose decode runs these ops as separate kernels
+ * (mamba2_block.cpp:84-290). */
+int lssm_inproj_ssd_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, const void* w,
+                           const void* w_scales, void* conv_state, const void* conv_w,
+                           const void* conv_b, const void* dt_bias, const void* A_log,
+                           const void* D_skip, float* ssd_state, void* y, uint64_t* xfer,
+                           uint32_t tag, uint32_t d_model, uint32_t d_inner, uint32_t d_state,
+                           uint32_t n_groups, uint32_t n_heads, uint32_t d_head, uint32_t d_conv,
+                           float eps, lssm_wfmt wfmt, lssm_dtype act);
+
 /* hidden[i, :] = table[ids[i], :]  (Mamba2Model::embed, mamba2_model.cpp:128-137). */
 int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out,
                uint32_t n, uint32_t d_model, uint32_t vocab, lssm_dtype act);
@@ -340,6 +361,11 @@ int lssm_engine_decode_graph(lssm_engine* e, const int32_t* ids, uint32_t batch,
 int lssm_engine_logits(lssm_engine* e, void** logits);          /* [max_batch, vocab] act */
 int lssm_engine_state(lssm_engine* e, void** conv_state, void** ssd_state);
 /* conv_state: [n_layer, max_batch, xBC_dim, d_conv] act; ssd: [n_layer, max_batch, H, P, N] f32 */
+/* Layers of the last decode step (eager or captured) whose SSD step ran inside
+ * the in_proj launch (batch 1; the environment variable LSSM_FUSED_SSD=0 at
+ * engine creation turns that off).  No counterpart in the reference, whose
+ * decode runs every op as its own kernel. */
+int lssm_engine_fused_layers(lssm_engine* e, uint32_t* layers);
 
 #ifdef __cplusplus
 }

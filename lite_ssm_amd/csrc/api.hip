@@ -285,6 +285,42 @@ int lssm_inproj_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, co
     return finish(ctx, "inproj_decode");
 }
 
+int lssm_inproj_ssd_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w, const void* w,
+                           const void* w_scales, void* conv_state, const void* conv_w,
+                           const void* conv_b, const void* dt_bias, const void* A_log,
+                           const void* D_skip, float* ssd_state, void* y, uint64_t* xfer,
+                           uint32_t tag, uint32_t d_model, uint32_t d_inner, uint32_t d_state,
+                           uint32_t n_groups, uint32_t n_heads, uint32_t d_head, uint32_t d_conv,
+                           float eps, lssm_wfmt wfmt, lssm_dtype act) {
+    LSSM_CHECK_CTX(ctx);
+    LSSM_REQUIRE(valid_act(act), "inproj_ssd_decode: unknown dtype");
+    if (int rc = check_fmt_k(d_model, wfmt, w_scales)) return rc;
+    LSSM_REQUIRE(xfer && ssd_state && y && norm_w && A_log && dt_bias, "inproj_ssd_decode: null pointer");
+    LSSM_REQUIRE(n_heads >= 1 && n_groups >= 1 && d_inner == n_heads * d_head,
+                 "inproj_ssd_decode: d_inner must equal n_heads * d_head");
+    const uint32_t xbc = d_inner + 2u * n_groups * d_state;
+    InprojDecodeArgs a;
+    a.g = GemvArgs{hidden, d_model, w, w_scales, nullptr, 0, nullptr, norm_w, eps, 1u,
+                   d_inner + xbc + n_heads, d_model, wfmt, act, LSSM_EPI_NONE};
+    a.d_inner = d_inner;
+    a.xbc = xbc;
+    a.H = n_heads;
+    a.dconv = d_conv;
+    a.conv_state = conv_state;
+    a.conv_w = conv_w;
+    a.conv_b = conv_b;
+    a.z = nullptr;
+    a.xbc_act = nullptr;
+    a.dt = nullptr;
+    const SsdFuseArgs f{xfer, nullptr, tag, ssd_state, A_log, dt_bias, D_skip, y, d_head, d_state, n_groups,
+                        1e-6f, 1e6f};
+    hipError_t e = hipSuccess;
+    if (!launch_inproj_ssd_decode(ctx->stream, a, f, e))
+        return set_error(LSSM_EINVAL, "inproj_ssd_decode: shape, format, alignment or grid not supported by the fused launch");
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "inproj_ssd_decode: %s", hipGetErrorString(e));
+    return finish(ctx, "inproj_ssd_decode");
+}
+
 int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out, uint32_t n,
                uint32_t d_model, uint32_t vocab, lssm_dtype act) {
     LSSM_CHECK_CTX(ctx);

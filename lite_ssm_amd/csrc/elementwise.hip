@@ -353,7 +353,9 @@ __global__ void conv1d_seed_kernel(const T* __restrict__ xBC, uint32_t xs, T* __
 // API rejects them before launch; this only guards the device read).
 template <typename T>
 __global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restrict__ ids,
-                             T* __restrict__ out, uint32_t n, uint32_t d_model, uint32_t vocab) {
+                             T* __restrict__ out, uint32_t n, uint32_t d_model, uint32_t vocab,
+                             uint32_t* __restrict__ seq) {
+    if (seq != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *seq += 1u;
     const size_t total = (size_t)n * d_model;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (size_t)gridDim.x * blockDim.x) {
@@ -601,13 +603,13 @@ hipError_t launch_conv1d_keep_last(hipStream_t s, void* state, uint32_t n_window
 }
 
 hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, void* out, uint32_t n,
-                        uint32_t d_model, uint32_t vocab, int act) {
+                        uint32_t d_model, uint32_t vocab, int act, uint32_t* seq) {
     if (n == 0) return hipSuccess;
     const size_t total = (size_t)n * d_model;
     const unsigned blocks = (unsigned)((total + NT - 1) / NT < 65536 ? (total + NT - 1) / NT : 65536);
     LSSM_DISPATCH_ACT(act, T,
                       embed_kernel<T><<<blocks, NT, 0, s>>>((const T*)table, ids, (T*)out, n,
-                                                            d_model, vocab));
+                                                            d_model, vocab, seq));
     return hipGetLastError();
 }
 

@@ -13,6 +13,7 @@
 //     no host round trip and can be captured once into a HIP graph.
 // Every intermediate is rounded at the same points as the reference's
 // unfused kernels.
+#include <cstdlib>
 #include <vector>
 
 #include "internal.hpp"
@@ -59,6 +60,14 @@ struct lssm_engine {
     void* conv_state = nullptr;
     float* ssd_state = nullptr;
     void* argmax_scratch = nullptr;
+    // batch-1 decode: in_proj and the SSD step in one launch (tagged words of
+    // each layer's projection; the tag is a step counter the embedding
+    // advances).  Both are zeroed once at creation and never reset together
+    // with a live tag.  LSSM_FUSED_SSD=0 in the environment turns it off.
+    uint64_t* xfer = nullptr;
+    uint32_t* seq = nullptr;
+    bool fuse_ssd = true;
+    mutable uint32_t fused_layers = 0;   // of the last decode step issued
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -121,16 +130,18 @@ struct lssm_engine {
 
     // One decode step: ids -> next (all on device).  mamba2_block.cpp:317-327.
     hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
-        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act);
+        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act, fuse_ssd ? seq : nullptr);
         // fused RMSNorm + linear kernels: the VALU GEMV up to 4 rows, the MFMA
         // GEMV for decode batches of the shapes it takes
         const bool fused_in = (B <= 4 && (int)B <= gemv_max_rows(d_model, wfmt, act)) ||
                               (B >= 2 && gemv_mma_takes(B, proj, d_model, wfmt, act));
         const bool fused_out = (B <= 4 && gemv_max_rows(d_inner, wfmt, act) >= 1) ||
                                (B >= 2 && gemv_mma_takes(B, d_model, d_inner, wfmt, act));
+        fused_layers = 0;
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
             char* cs = conv_layer(li);
+            bool ssd_done = false;   // the SSD step ran inside the in_proj launch
             if (fused_in) {
                 InprojDecodeArgs a;
                 a.g = GemvArgs{d_hidden, d_model, w.in_proj_w, w.in_proj_s, nullptr, 0, nullptr,
@@ -145,7 +156,13 @@ struct lssm_engine {
                 a.z = d_z;
                 a.xbc_act = d_xbc;
                 a.dt = d_dt;
-                e = launch_inproj_decode(st(), a);
+                if (B == 1 && fuse_ssd) {
+                    const SsdFuseArgs f{xfer + (size_t)li * proj, seq, 0u, ssd_layer(li), w.A_log, w.dt_bias, w.D,
+                                        d_g, P, N, G, DT_MIN, DT_MAX};
+                    ssd_done = launch_inproj_ssd_decode(st(), a, f, e);
+                    fused_layers += ssd_done ? 1u : 0u;
+                }
+                if (!ssd_done) e = launch_inproj_decode(st(), a);
             } else {
                 e = launch_rmsnorm(st(), d_hidden, d_model, w.norm_w, d_normed, d_model, B, d_model,
                                    RMS_EPS, act);
@@ -166,7 +183,7 @@ struct lssm_engine {
                       (char*)d_xbc + (size_t)(d_inner + GN) * es, xbc, dt, dts, w.dt_bias, w.A_log,
                       w.D, d_g, d_inner, ssd_layer(li), B, 1, H, P, N, G, 1, DT_MIN, DT_MAX, 1u, act,
                       z, zs};
-            e = launch_ssd_step(st(), s);
+            if (!ssd_done) e = launch_ssd_step(st(), s);
             if (e != hipSuccess) break;
             if (fused_out) {
                 GemvArgs g{d_g, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden,
@@ -356,6 +373,15 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A(&e->conv_state, (size_t)cfg->n_layer * max_batch * e->xbc * e->K * es);
     A((void**)&e->ssd_state, (size_t)cfg->n_layer * max_batch * e->H * e->P * e->N * sizeof(float));
     A(&e->argmax_scratch, (size_t)max_batch * 128 * 8);
+    const size_t xfer_bytes = (size_t)cfg->n_layer * e->proj * sizeof(uint64_t);
+    A((void**)&e->xfer, xfer_bytes);
+    A((void**)&e->seq, 256);
+    if (rc == LSSM_OK) {
+        hipError_t err = hipMemsetAsync(e->xfer, 0, xfer_bytes, ctx->stream);
+        if (err == hipSuccess) err = hipMemsetAsync(e->seq, 0, 256, ctx->stream);
+        if (err != hipSuccess) rc = set_error(LSSM_EDEVICE, "engine_create: %s", hipGetErrorString(err));
+    }
+    if (const char* v = getenv("LSSM_FUSED_SSD")) e->fuse_ssd = v[0] != '0';
     if (rc != LSSM_OK) {
         delete e;
         return rc;
@@ -439,6 +465,13 @@ int lssm_engine_logits(lssm_engine* e, void** logits) {
     if (int rc = check_engine(e)) return rc;
     LSSM_REQUIRE(logits, "engine_logits: null out");
     *logits = e->logits;
+    return LSSM_OK;
+}
+
+int lssm_engine_fused_layers(lssm_engine* e, uint32_t* layers) {
+    if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(layers, "engine_fused_layers: null out");
+    *layers = e->fused_layers;
     return LSSM_OK;
 }
 

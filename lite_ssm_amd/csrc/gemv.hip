@@ -36,6 +36,159 @@ namespace lssm {
 namespace {
 
 
+// ---------------------------------------------------------------------------
+// Engine decode at batch 1: in_proj + conv + SSD step in one launch
+// ---------------------------------------------------------------------------
+// The in_proj epilogue (EpiInproj::value) publishes every output row as one
+// 64-bit word, (value bits) | (step tag << 32), written by a single-copy-atomic
+// device-coherent store; a reader on any CU takes a word once its tag is this
+// step's, so neither a fence nor a counter is needed (the tag is a step
+// counter the embedding kernel advances; each layer has its own words).
+// After its rows, block b runs the SSD step + SiLU(z) gate of the (head,
+// 32-column) items b, b + grid, ... with ssd_step_kernel's arithmetic
+// (ssd_step.metal:33-77): it waits for the 2N + 65 words an item reads (B and
+// C of the head's group, x and z of its columns, dt of the head), which other
+// blocks of the same launch store.  The launcher fuses only when every block
+// of the launch is resident at once (at most one block per CU), so every
+// awaited word gets written; the wait is bounded all the same, and a column
+// whose words never arrive gets a NaN output.
+template <typename T> struct EpiInprojSsd {
+    static constexpr bool kNormOptional = false;
+    static constexpr bool kTail = true;
+    static constexpr uint32_t IP = 32;                    // state columns per item
+    static constexpr uint32_t NV = 8;                     // lanes per column
+    static constexpr uint32_t NN = 128;                   // d_state
+    static constexpr int F = (int)(NN / (4 * NV));        // 16-byte state pieces per lane
+    static constexpr uint32_t NWD = 2 * NN + 2 * IP + 1;  // words an item reads
+    static constexpr uint32_t SPIN = 1u << 16;            // polls before giving up
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    EpiInproj<T> in;                                      // routing / conv (its z, xbc_act, dt unused)
+    uint64_t* xfer;                                       // [proj] tagged words of this layer
+    const uint32_t* seq;                                  // the step tag (device), or null:
+    uint32_t tag0;                                        //   this one
+    float* state;                                         // [H, P, NN] of this layer
+    const T* A_log;
+    const T* dt_bias;
+    const T* D;                                           // nullptr: no D term
+    T* y;                                                 // [d_inner] gated SSD output
+    uint32_t P, G, items;                                 // items = H * P / IP
+    float dt_min, dt_max;
+    using Pre = typename EpiInproj<T>::Pre;
+    struct Early {
+        f32x4 s[F];
+        uint32_t alr, dbr, dr;
+    };
+    __device__ __forceinline__ void pin() const {
+        in.pin();
+        pin_arg(xfer);
+        pin_arg(seq);
+        pin_arg(tag0);
+        pin_arg(state);
+        pin_arg(A_log);
+        pin_arg(dt_bias);
+        pin_arg(D);
+        pin_arg(P);
+        pin_arg(items);
+    }
+    __device__ __forceinline__ Pre prefetch(int m, uint32_t n) const { return in.prefetch(m, n); }
+    __device__ __forceinline__ void operator()(int m, uint32_t n, float acc, const Pre& p) const {
+        const T v = in.value(m, n, acc, p);
+        const uint64_t word = (uint64_t)bits16(v) | ((uint64_t)(seq ? *seq : tag0) << 32);
+        __hip_atomic_store(xfer + n, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // The state columns and head scalars of the block's first item, requested
+    // right behind the weights (every thread loads: clamped, values unused
+    // where there is no item).
+    __device__ __forceinline__ Early early() const {
+        Early e;
+        const uint32_t it = blockIdx.x < items ? blockIdx.x : items - 1;
+        const uint32_t t = threadIdx.x % (IP * NV);
+        const uint32_t ipp = P / IP, h = it / ipp, p = (it % ipp) * IP + t / NV;
+        const f32x4* S = reinterpret_cast<const f32x4*>(state + ((size_t)h * P + p) * NN);
+#pragma unroll
+        for (int f = 0; f < F; ++f) e.s[f] = S[t % NV + NV * f];
+        e.alr = raw_at(A_log + h);
+        e.dbr = raw_at(dt_bias + h);
+        e.dr = raw_at(D ? D + h : A_log + h);             // value unused without D
+        return e;
+    }
+    __device__ __forceinline__ void tail(const Early& e) const {
+        __shared__ uint32_t wv[NWD];                      // B, C, x, z, dt value bits
+        constexpr uint32_t QNAN = __is_same(T, f16) ? 0x7E00u : 0x7FC0u;
+        const uint32_t tag = seq ? *seq : tag0;
+        const uint32_t d_inner = in.d_inner, H = in.H, GN = G * NN, ipp = P / IP;
+        for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
+            const uint32_t h = it / ipp, p0 = (it % ipp) * IP, g = h / (H / G);
+            __syncthreads();                              // the previous item's words read
+            for (uint32_t t = threadIdx.x; t < NWD; t += blockDim.x) {
+                uint32_t idx;
+                if (t < NN) idx = 2 * d_inner + g * NN + t;                              // B
+                else if (t < 2 * NN) idx = 2 * d_inner + GN + g * NN + (t - NN);         // C
+                else if (t < 2 * NN + IP) idx = d_inner + h * P + p0 + (t - 2 * NN);     // x
+                else if (t < 2 * NN + 2 * IP) idx = h * P + p0 + (t - 2 * NN - IP);      // z
+                else idx = d_inner + in.xbc + h;                                         // dt
+                uint64_t v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (uint32_t n = 0; (uint32_t)(v >> 32) != tag && n < SPIN; ++n)
+                    v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wv[t] = (uint32_t)(v >> 32) == tag ? (uint32_t)v : QNAN;
+            }
+            __syncthreads();
+            if (threadIdx.x < IP * NV) {                  // wave-uniform
+                const uint32_t lr = threadIdx.x % NV, pl = threadIdx.x / NV;
+                f32x4* S = reinterpret_cast<f32x4*>(state + ((size_t)h * P + p0 + pl) * NN);
+                f32x4 s[F];
+                uint32_t alr = e.alr, dbr = e.dbr, dr = e.dr;
+                if (it == blockIdx.x) {
+#pragma unroll
+                    for (int f = 0; f < F; ++f) s[f] = e.s[f];
+                } else {
+#pragma unroll
+                    for (int f = 0; f < F; ++f) s[f] = S[lr + NV * f];
+                    alr = raw_at(A_log + h);
+                    dbr = raw_at(dt_bias + h);
+                    dr = raw_at(D ? D + h : A_log + h);
+                }
+                const float xv = f_of_raw<T>(wv[2 * NN + pl]);
+                const float A_h = -expf(f_of_raw<T>(alr));
+                float dt = softplus_f(f_of_raw<T>(wv[2 * NN + 2 * IP]) + f_of_raw<T>(dbr));
+                dt = fminf(fmaxf(dt, dt_min), dt_max);
+                const float decay = expf(A_h * dt);
+                float ys = 0.0f;
+#pragma unroll
+                for (int f = 0; f < F; ++f) {
+                    const uint32_t n0 = 4 * (lr + NV * f);
+                    const float b0 = f_of_raw<T>(wv[n0]), b1 = f_of_raw<T>(wv[n0 + 1]);
+                    const float b2 = f_of_raw<T>(wv[n0 + 2]), b3 = f_of_raw<T>(wv[n0 + 3]);
+                    const float c0 = f_of_raw<T>(wv[NN + n0]), c1 = f_of_raw<T>(wv[NN + n0 + 1]);
+                    const float c2 = f_of_raw<T>(wv[NN + n0 + 2]), c3 = f_of_raw<T>(wv[NN + n0 + 3]);
+                    // the same fused multiply-adds as ssd_step_kernel
+                    f32x4 t = s[f];
+                    t.x = fmaf(decay, t.x, dt * b0 * xv);
+                    t.y = fmaf(decay, t.y, dt * b1 * xv);
+                    t.z = fmaf(decay, t.z, dt * b2 * xv);
+                    t.w = fmaf(decay, t.w, dt * b3 * xv);
+                    S[lr + NV * f] = t;
+                    ys += fmaf(c3, t.w, fmaf(c2, t.z, fmaf(c0, t.x, c1 * t.y)));
+                }
+                ys = group_sum<NV>(ys);
+                if (lr == 0) {
+                    float yv = rnd<T>(fmaf(D ? f_of_raw<T>(dr) : 0.0f, xv, ys));
+                    yv = silu_fast(f_of_raw<T>(wv[2 * NN + IP + pl])) * yv;
+                    y[(size_t)h * P + p0 + pl] = from_f<T>(yv);
+                }
+            }
+        }
+    }
+};
+
+// What a kTail epilogue loads behind the weights (nothing for the others).
+template <class Epi, bool = Epi::kTail> struct EarlyOf {
+    struct type {};
+};
+template <class Epi> struct EarlyOf<Epi, true> {
+    using type = typename Epi::Early;
+};
+
 // Weights, raw scale bits and epilogue inputs of the rows one wave handles.
 template <int CPL, int MR, class Epi> struct RowSet {
     uint4 wq[CPL];
@@ -237,6 +390,8 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
     // held for as long as the memory system pushes back, and no barrier may
     // wait on that.
     load_w(A);
+    [[maybe_unused]] typename EarlyOf<Epi>::type early{};
+    if constexpr (Epi::kTail) early = epi.early();
 
 
     // ---- 4. rows; the next row's loads are in flight while this one is reduced ----
@@ -293,6 +448,7 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
             compute(B);
         }
     }
+    if constexpr (Epi::kTail) epi.tail(early);
 }
 
 template <int FMT, typename T, int LPR, int CPL, int MR, class Epi>
@@ -323,6 +479,11 @@ hipError_t go1(hipStream_t s, const GemvCore& c, const Epi& e, int mr, int norm)
     const uint32_t blocks = (waves + wpb - 1) / wpb;
     const size_t lds = (size_t)MR * (KC / F::WPC) * xs_of<F::WPC / 2>() * sizeof(uint32_t);
     if (c.K != KC || lds > GV_LDS_MAX) return hipErrorInvalidValue;
+    // a tail that waits on other blocks' rows needs every block resident: one
+    // block per CU (up to 16 waves at <= 128 VGPRs fits an idle CU)
+    if constexpr (Epi::kTail) {
+        if (blocks > num_cus() || MR != 1) return hipErrorNotSupported;
+    }
     auto run = [&](auto k) -> hipError_t {
         // opt in to the full dynamic LDS once per instantiation (a host attribute)
         static const hipError_t attr = hipFuncSetAttribute(
@@ -682,6 +843,50 @@ hipError_t launch_inproj_decode(hipStream_t s, const InprojDecodeArgs& a) {
     if (g.act == LSSM_F16) return go(f16{});
     if (g.act == LSSM_BF16) return go(bf16{});
     return go(float{});
+}
+
+bool launch_inproj_ssd_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseArgs& f, hipError_t& err) {
+    err = hipSuccess;
+    const GemvArgs& g = a.g;
+    if (g.M != 1 || !g.norm_w || (g.act != LSSM_F16 && g.act != LSSM_BF16)) return false;
+    if (a.dconv != 4 || f.N != EpiInprojSsd<f16>::NN || f.P == 0 || f.P % EpiInprojSsd<f16>::IP != 0 ||
+        f.G == 0 || a.H % f.G != 0 || a.d_inner != a.H * f.P || a.xbc != a.d_inner + 2 * f.G * f.N ||
+        g.N != a.d_inner + a.xbc + a.H)
+        return false;
+    if (g.wfmt != LSSM_W_Q4_G64 && !(g.wfmt == LSSM_W_Q8_G32 && g.act == LSSM_F16)) return false;
+    const bool aligned = ((uintptr_t)g.x % 16 == 0) && ((uintptr_t)g.norm_w % 16 == 0) &&
+                         ((uintptr_t)g.w % 16 == 0) && ((uintptr_t)f.state % 16 == 0) &&
+                         ((uintptr_t)a.conv_state % 8 == 0) && ((uintptr_t)a.conv_w % 8 == 0);
+    if (!aligned || gemv1_rows(g.K, g.wfmt, g.act) < 1) return false;
+    GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
+    auto go = [&](auto tag) -> hipError_t {
+        using T = decltype(tag);
+        EpiInprojSsd<T> e{};
+        e.in = EpiInproj<T>{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,
+                            (const T*)a.conv_b, nullptr, nullptr, nullptr};
+        e.xfer = f.xfer;
+        e.seq = f.seq;
+        e.tag0 = f.tag;
+        e.state = f.state;
+        e.A_log = (const T*)f.A_log;
+        e.dt_bias = (const T*)f.dt_bias;
+        e.D = (const T*)f.D;
+        e.y = (T*)f.y;
+        e.P = f.P;
+        e.G = f.G;
+        e.items = a.H * (f.P / EpiInprojSsd<T>::IP);
+        e.dt_min = f.dt_min;
+        e.dt_max = f.dt_max;
+        bool done = false;
+        hipError_t r = hipErrorNotSupported;
+        if (g.wfmt == LSSM_W_Q4_G64) r = launch_gemv1<LSSM_W_Q4_G64, T, 1, EpiInprojSsd<T>>(s, c, e, 1, 1, done);
+        else if constexpr (__is_same(T, f16)) r = launch_gemv1<LSSM_W_Q8_G32, T, 1, EpiInprojSsd<T>>(s, c, e, 1, 1, done);
+        return done ? r : hipErrorNotSupported;
+    };
+    const hipError_t r = g.act == LSSM_F16 ? go(f16{}) : go(bf16{});
+    if (r == hipErrorNotSupported) return false;   // nothing launched
+    err = r;
+    return true;
 }
 
 hipError_t launch_dequant(hipStream_t s, const void* w, const void* sc, float* out, uint32_t N,

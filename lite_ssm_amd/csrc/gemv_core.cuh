@@ -85,6 +85,7 @@ template <typename V> __device__ __forceinline__ void pin_arg(const V& v) {
 // y[m, n] = r(acc) / r(silu(acc)) / r(res + r(acc))
 template <typename T> struct EpiPlain {
     static constexpr bool kNormOptional = true;
+    static constexpr bool kTail = false;             // no block-level work after the rows
     T* y;
     uint32_t y_stride;
     const T* res;
@@ -133,6 +134,7 @@ template <typename T> struct EpiPlain {
 // output is rounded once more before SiLU, as in the unfused op sequence.
 template <typename T> struct EpiInproj {
     static constexpr bool kNormOptional = false;           // always behind the layer RMSNorm
+    static constexpr bool kTail = false;
     uint32_t d_inner, xbc, H, dconv;
     T* conv_state;
     const T* conv_w;
@@ -174,46 +176,49 @@ template <typename T> struct EpiInproj {
         }
         return p;
     }
-    __device__ __forceinline__ void operator()(int m, uint32_t n, float acc, const Pre& p) const {
+    // The value row n takes: r(acc) for z and dt rows; for an xBC row the
+    // conv window is shifted (and written back) and silu(r(conv)) returned.
+    __device__ __forceinline__ T value(int m, uint32_t n, float acc, const Pre& p) const {
         const T v = from_f<T>(acc);
-        if (n < d_inner) {
-            z[(size_t)m * d_inner + n] = v;
-        } else if (n < d_inner + xbc) {
-            const uint32_t c = n - d_inner;
-            T* sd = conv_state + ((size_t)m * xbc + c) * dconv;
-            float a = 0.0f;
-            bool done = false;
-            if constexpr (kVec) {
-                if (dconv == 4) {
-                    // taps and weights by bit extraction (an address of the
-                    // registers would put them in scratch)
-                    auto lo = [](uint32_t d) { return f_of_raw<T>(d & 0xFFFFu); };
-                    auto hi = [](uint32_t d) { return f_of_raw<T>(d >> 16); };
-                    // window shift (conv1d.metal:127-130): taps 1..3 move down, x lands in 3
-                    a = f_of_raw<T>(p.b) + hi(p.s.x) * lo(p.w.x) + lo(p.s.y) * hi(p.w.x) +
-                        hi(p.s.y) * lo(p.w.y) + to_f(v) * hi(p.w.y);
-                    uint2 ns;
-                    ns.x = p.s.x >> 16 | p.s.y << 16;                                     // (s1, s2)
-                    ns.y = p.s.y >> 16 | (uint32_t)__builtin_bit_cast(uint16_t, v) << 16;  // (s3, x)
-                    *reinterpret_cast<uint2*>(sd) = ns;
-                    done = true;
-                }
+        if (n < d_inner || n >= d_inner + xbc) return v;
+        const uint32_t c = n - d_inner;
+        T* sd = conv_state + ((size_t)m * xbc + c) * dconv;
+        float a = 0.0f;
+        bool done = false;
+        if constexpr (kVec) {
+            if (dconv == 4) {
+                // taps and weights by bit extraction (an address of the
+                // registers would put them in scratch)
+                auto lo = [](uint32_t d) { return f_of_raw<T>(d & 0xFFFFu); };
+                auto hi = [](uint32_t d) { return f_of_raw<T>(d >> 16); };
+                // window shift (conv1d.metal:127-130): taps 1..3 move down, x lands in 3
+                a = f_of_raw<T>(p.b) + hi(p.s.x) * lo(p.w.x) + lo(p.s.y) * hi(p.w.x) +
+                    hi(p.s.y) * lo(p.w.y) + to_f(v) * hi(p.w.y);
+                uint2 ns;
+                ns.x = p.s.x >> 16 | p.s.y << 16;                                     // (s1, s2)
+                ns.y = p.s.y >> 16 | (uint32_t)__builtin_bit_cast(uint16_t, v) << 16;  // (s3, x)
+                *reinterpret_cast<uint2*>(sd) = ns;
+                done = true;
             }
-            if (!done) {
-                const T* wd = conv_w + (size_t)c * dconv;
-                a = to_f(conv_b[c]);
-                for (uint32_t k = 0; k + 1 < dconv; ++k) {
-                    const T sk = sd[k + 1];
-                    sd[k] = sk;
-                    a += to_f(sk) * to_f(wd[k]);
-                }
-                sd[dconv - 1] = v;
-                a += to_f(v) * to_f(wd[dconv - 1]);
-            }
-            xbc_act[(size_t)m * xbc + c] = from_f<T>(silu_fast(rnd<T>(a)));
-        } else {
-            dt[(size_t)m * H + (n - d_inner - xbc)] = v;
         }
+        if (!done) {
+            const T* wd = conv_w + (size_t)c * dconv;
+            a = to_f(conv_b[c]);
+            for (uint32_t k = 0; k + 1 < dconv; ++k) {
+                const T sk = sd[k + 1];
+                sd[k] = sk;
+                a += to_f(sk) * to_f(wd[k]);
+            }
+            sd[dconv - 1] = v;
+            a += to_f(v) * to_f(wd[dconv - 1]);
+        }
+        return from_f<T>(silu_fast(rnd<T>(a)));
+    }
+    __device__ __forceinline__ void operator()(int m, uint32_t n, float acc, const Pre& p) const {
+        const T v = value(m, n, acc, p);
+        if (n < d_inner) z[(size_t)m * d_inner + n] = v;
+        else if (n < d_inner + xbc) xbc_act[(size_t)m * xbc + (n - d_inner)] = v;
+        else dt[(size_t)m * H + (n - d_inner - xbc)] = v;
     }
     // four rows m[0..3] of one channel n: the conv weights and bias once
     struct Pre4 {

@@ -86,8 +86,10 @@ hipError_t launch_conv1d_keep_last(hipStream_t s, void* state, uint32_t n_window
                                    int act);
 hipError_t launch_conv1d_seed(hipStream_t s, const void* xBC, uint32_t x_stride, void* state,
                               uint32_t B, uint32_t L, uint32_t D, uint32_t K, int act);
+// seq (optional): a step counter the kernel advances by one (the tag of the
+// fused decode launch's words).
 hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, void* out,
-                        uint32_t n, uint32_t d_model, uint32_t vocab, int act);
+                        uint32_t n, uint32_t d_model, uint32_t vocab, int act, uint32_t* seq = nullptr);
 hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32_t rows,
                          uint32_t vocab, int act, void* scratch);
 
@@ -170,6 +172,26 @@ struct InprojDecodeArgs {
     void* dt;             // [B, H]
 };
 hipError_t launch_inproj_decode(hipStream_t s, const InprojDecodeArgs& a);
+
+// Engine decode at batch 1: launch_inproj_decode's rows, published as tagged
+// words, and the layer's SSD step + SiLU(z) gate (ssd_step_kernel's
+// arithmetic) in the same launch; z / xbc_act / dt of `a` are not written.
+// Returns false (launching nothing) when the shape, format, alignment or grid
+// is not one it takes; err holds the launch result.
+struct SsdFuseArgs {
+    uint64_t* xfer;          // [proj] tagged words of this layer (zeroed once)
+    const uint32_t* seq;     // step tag in device memory, advanced once per decode
+                             // step (launch_embed); null: `tag` below
+    uint32_t tag;
+    float* state;            // [H, P, N] fp32
+    const void* A_log;
+    const void* dt_bias;
+    const void* D;           // may be null
+    void* y;                 // [d_inner]
+    uint32_t P, N, G;
+    float dt_min, dt_max;
+};
+bool launch_inproj_ssd_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseArgs& f, hipError_t& err);
 
 // MFMA GEMV for decode batches (gemv_mma.hip): 2..64 rows, GEMV rule, RMSNorm
 // prologue when norm_w is set.  Returns false (launching nothing) when the

@@ -82,17 +82,19 @@ __global__ __launch_bounds__(ST_NT) void ssd_step_kernel(SsdArgs a) {
 #pragma unroll
     for (int f = 0; f < F; ++f) {
         // s = decay*s + (dt*B)*x  (ssd_step.metal:68-69)
+        // the fused multiply-adds are spelled out: the batch-1 decode launch
+        // that also runs this step (gemv.hip) must round identically
         f32x4 t = s[f];
-        t.x = decay * t.x + dt * to_f(bv[f].x) * xv;
-        t.y = decay * t.y + dt * to_f(bv[f].y) * xv;
-        t.z = decay * t.z + dt * to_f(bv[f].z) * xv;
-        t.w = decay * t.w + dt * to_f(bv[f].w) * xv;
+        t.x = fmaf(decay, t.x, dt * to_f(bv[f].x) * xv);
+        t.y = fmaf(decay, t.y, dt * to_f(bv[f].y) * xv);
+        t.z = fmaf(decay, t.z, dt * to_f(bv[f].z) * xv);
+        t.w = fmaf(decay, t.w, dt * to_f(bv[f].w) * xv);
         S[lr + ST_NV * f] = t;
-        ys += to_f(cv[f].x) * t.x + to_f(cv[f].y) * t.y + to_f(cv[f].z) * t.z + to_f(cv[f].w) * t.w;
+        ys += fmaf(to_f(cv[f].w), t.w, fmaf(to_f(cv[f].z), t.z, fmaf(to_f(cv[f].x), t.x, to_f(cv[f].y) * t.y)));
     }
     ys = group_sum<ST_NV>(ys);
     if (lr == 0) {
-        float y = rnd<T>(ys + (a.has_D ? f_of<T>(dr) : 0.0f) * xv);
+        float y = rnd<T>(fmaf(a.has_D ? f_of<T>(dr) : 0.0f, xv, ys));
         if constexpr (GATE) y = silu_fast(f_of<T>(zr)) * y;
         ((T*)a.Y)[(size_t)b * a.y_stride + (size_t)h * P + p] = from_f<T>(y);
     }

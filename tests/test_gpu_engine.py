@@ -224,3 +224,67 @@ def test_engine_argument_errors(ctx):
     with pytest.raises(L.LssmError, match="batch out of range"):
         eng.decode(torch.zeros(2, dtype=torch.int32, device="cuda"), nxt)
     eng.close()
+
+
+FUSED_CASES = [
+    ("2.7b-bf16-q4g64", "mamba2-2.7b", O.BF16, O.W_Q4_G64, dict(n_layer=2, vocab_size=512)),
+    ("130m-f16-q8g32", "mamba2-130m", O.F16, O.W_Q8_G32, dict(n_layer=2, vocab_size=1024)),
+]
+
+
+@pytest.mark.parametrize("tag,name,act,wfmt,over", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
+def test_engine_fused_ssd_decode_bs1(ctx, tag, name, act, wfmt, over):
+    """Batch-1 decode with the SSD step inside the in_proj launch (tagged words
+    read across CUs): bit-identical to the three-launch decode
+    (LSSM_FUSED_SSD=0) on every step, eager and graph-replayed (the step tag
+    advances inside the graph), and within tolerance of the oracle."""
+    import os
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, name, act, wfmt, **over)
+    Lq = 40
+    fused = Engine(ctx, m, max_batch=1, max_seq=Lq)
+    os.environ["LSSM_FUSED_SSD"] = "0"
+    try:
+        plain = Engine(ctx, m, max_batch=1, max_seq=Lq)
+    finally:
+        del os.environ["LSSM_FUSED_SSD"]
+    try:
+        _fused_vs_plain(tag, sh, om, act, fused, plain, Lq)
+    finally:
+        fused.close()
+        plain.close()
+
+
+def _fused_vs_plain(tag, sh, om, act, fused, plain, Lq):
+    ids = np.random.default_rng(7).integers(0, sh.vocab_size, (1, Lq)).astype(np.int32)
+    n_f = torch.zeros(1, dtype=torch.int32, device="cuda")
+    n_p = torch.zeros_like(n_f)
+    fused.prefill(torch.from_numpy(ids).cuda(), n_f)
+    plain.prefill(torch.from_numpy(ids).cuda(), n_p)
+    conv, ssd = om.new_state(1)
+    ref = om.prefill(conv, ssd, ids)
+    tok = O.argmax(ref, act)
+
+    def same(step):
+        assert torch.equal(fused.logits(1), plain.logits(1)), f"{tag} logits, step {step}"
+        cf, sf = fused.state()
+        cp, sp = plain.state()
+        assert torch.equal(sf, sp) and torch.equal(cf, cp), f"{tag} state, step {step}"
+
+    for step in range(4):
+        t = torch.from_numpy(tok).cuda()
+        fused.decode(t, n_f)
+        plain.decode(t, n_p)
+        assert fused.fused_layers() == sh.n_layer and plain.fused_layers() == 0
+        same(step)
+        ref = om.decode(conv, ssd, tok)
+        _check_logits(fused.logits(1).float().cpu().numpy(), ref, act, f"{tag} decode {step}")
+        tok = O.argmax(ref, act)
+    t_f = torch.from_numpy(tok).cuda()
+    t_p = t_f.clone()
+    fused.decode_graph(t_f, t_f, 6)
+    for _ in range(6):
+        plain.decode(t_p, t_p)
+    assert fused.fused_layers() == sh.n_layer
+    assert torch.equal(t_f, t_p)
+    same("graph")

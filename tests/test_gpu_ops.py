@@ -448,6 +448,76 @@ def test_inproj_decode_vs_unfused_chain(ctx, rng, act, wfmt, batch, d_model):
     assert_close(act_host(csd, act), cs2, act, bound, "conv_state")
 
 
+INPROJ_SSD_CASES = [
+    # d_model, d_inner, N, G, H, act, wfmt: 2.7B (int4-g64 bf16), 130M (int8-g32 fp16),
+    # a 2-group int4 fp16 shape
+    (2560, 5120, 128, 1, 80, O.BF16, O.W_Q4_G64), (768, 1536, 128, 1, 24, O.F16, O.W_Q8_G32),
+    (2048, 2048, 128, 2, 32, O.F16, O.W_Q4_G64),
+]
+
+
+@pytest.mark.parametrize("d_model,d_inner,N,G,H,act,wfmt", INPROJ_SSD_CASES,
+                         ids=[f"dm{c[0]}-h{c[4]}-g{c[3]}" for c in INPROJ_SSD_CASES])
+def test_inproj_ssd_decode_vs_unfused_chain(ctx, rng, d_model, d_inner, N, G, H, act, wfmt):
+    """Batch-1 in_proj + conv + SSD step + SiLU(z) gate in one launch (rows passed
+    between workgroups as tagged words): conv and SSD state bit-identical to
+    lssm_inproj_decode -> lssm_ssd_step, y within rounding of r(silu(z) r(y));
+    two calls in a row on the same word buffer (tags 1, 2)."""
+    import lite_ssm_amd as L
+    P, K = d_inner // H, 4
+    xbc = d_inner + 2 * G * N
+    proj = d_inner + xbc + H
+    nw = dev(O.to_act(1 + 0.1 * rng.standard_normal(d_model), act))
+    w, s = _weights(rng, proj, d_model, wfmt, act)
+    w, s = dev(w), None if s is None else dev(s)
+    cw = dev(O.to_act(rng.standard_normal((xbc, K)) * 0.3, act))
+    cb = dev(O.to_act(rng.standard_normal(xbc) * 0.1, act))
+    dtb = dev(O.to_act(rng.standard_normal(H) * 0.5, act))
+    alog = dev(O.to_act(rng.uniform(0, np.log(16), H), act))
+    Dh = dev(O.to_act(rng.standard_normal(H), act))
+    cs0 = O.to_act(rng.standard_normal((1, xbc, K)), act)
+    st0 = (rng.standard_normal((H, P, N)) * 0.1).astype(np.float32)
+    cs_f, cs_u = dev(cs0), dev(cs0)
+    st_f, st_u = dev(st0), dev(st0)
+    xfer = torch.zeros(proj, dtype=torch.int64, device="cuda")
+    z, xa, dt = empty((1, d_inner), act), empty((1, xbc), act), empty((1, H), act)
+    y_f, y_u = empty((1, d_inner), act), empty((1, d_inner), act)
+    dims = L.SSDStepDims(H, P, N, G, 1e-6, 1e6, 1)
+    for tag in (1, 2):
+        hid = dev(O.to_act(rng.standard_normal((1, d_model)) * 0.5, act))
+        L.check(L.lib.lssm_inproj_ssd_decode(
+            ctx.h, hid.data_ptr(), nw.data_ptr(), w.data_ptr(), None if s is None else s.data_ptr(),
+            cs_f.data_ptr(), cw.data_ptr(), cb.data_ptr(), dtb.data_ptr(), alog.data_ptr(), Dh.data_ptr(),
+            st_f.data_ptr(), y_f.data_ptr(), xfer.data_ptr(), tag, d_model, d_inner, N, G, H, P, K,
+            1e-5, wfmt, act))
+        L.check(L.lib.lssm_inproj_decode(
+            ctx.h, hid.data_ptr(), nw.data_ptr(), w.data_ptr(), None if s is None else s.data_ptr(),
+            cs_u.data_ptr(), cw.data_ptr(), cb.data_ptr(), z.data_ptr(), xa.data_ptr(), dt.data_ptr(),
+            1, d_model, d_inner, N, G, H, K, 1e-5, wfmt, act))
+        es = xa.element_size()
+        L.check(L.lib.lssm_ssd_step(ctx.h, xa.data_ptr(), xa.data_ptr() + d_inner * es,
+                                    xa.data_ptr() + (d_inner + G * N) * es, dt.data_ptr(), dtb.data_ptr(),
+                                    alog.data_ptr(), Dh.data_ptr(), st_u.data_ptr(), y_u.data_ptr(), 1, dims, act))
+        torch.cuda.synchronize()
+        assert torch.equal(cs_f, cs_u), f"conv state, tag {tag}"
+        assert torch.equal(st_f, st_u), f"ssd state, tag {tag}"
+        zf = O.from_act(act_host(z, act), act).astype(np.float64)
+        yu = O.from_act(act_host(y_u, act), act).astype(np.float64)
+        ref = O.to_act(zf / (1 + np.exp(-zf)) * yu, act)
+        assert_close(act_host(y_f, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2}[act], f"y, tag {tag}")
+
+
+def test_inproj_ssd_decode_rejects_unsupported(ctx):
+    """Shapes the fused launch does not take are refused with nothing run."""
+    import lite_ssm_amd as L
+    dummy = torch.zeros(1 << 16, dtype=torch.int64, device="cuda")
+    p = dummy.data_ptr()
+    # d_state 64 (the fused tail is built for 128)
+    rc = L.lib.lssm_inproj_ssd_decode(ctx.h, p, p, p, p, p, p, p, p, p, p, p, p, p, 1,
+                                      2560, 5120, 64, 1, 80, 64, 4, 1e-5, O.W_Q4_G64, O.BF16)
+    assert rc == 1 and b"not supported" in L.lib.lssm_last_error()
+
+
 NORM_LINEAR_CASES = [
     # rows, N, K, act, wfmt, epi: 2.7B out_proj (K 5120: 16 rows in two passes),
     # 8B out_proj (K 8192), odd N, the VALU GEMV rows (1, 3) and the fallback
