@@ -301,6 +301,29 @@ int lssm_inproj_ssd_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w
                            uint32_t n_groups, uint32_t n_heads, uint32_t d_head, uint32_t d_conv,
                            float eps, lssm_wfmt wfmt, lssm_dtype act);
 
+/* Batch-1 decode of one layer's whole mixer in ONE launch (in place on
+ * `hidden` [d_model]): lssm_inproj_ssd_decode, then r(gated RMSNorm(y)) (the
+ * mixer norm, norm.metal:52-79), out_proj and the residual add, hidden =
+ * r(hidden + r(y_n . deq(W_out)^T)): bit-identical to lssm_inproj_ssd_decode ->
+ * lssm_norm_linear_decode(..., EPI_ADD).  `xfer` holds d_inner + xBC_dim +
+ * n_heads + d_inner 64-bit words (projection rows, then the gated SSD outputs
+ * as 32-bit words carrying the tag modulo 2^16), zeroed before first use;
+ * `tag` must differ from the previous call's tag on the same `xfer` modulo
+ * 2^16 (a step counter does).  Both
+ * projections use `wfmt`.  Takes the shapes of lssm_inproj_ssd_decode whose
+ * (d_model, d_inner) it is built for: int4-g64 (2560, 5120) and (2048, 2048),
+ * int8-g32 fp16 (768, 1536); others return LSSM_EINVAL (nothing runs).  No
+ * counterpart in the reference (mamba2_block.cpp:84-290 runs these as
+ * separate kernels). */
+int lssm_mixer_decode(lssm_ctx* ctx, void* hidden, const void* norm_w, const void* in_w,
+                      const void* in_scales, void* conv_state, const void* conv_w,
+                      const void* conv_b, const void* dt_bias, const void* A_log,
+                      const void* D_skip, float* ssd_state, const void* mixer_norm_w,
+                      const void* out_w, const void* out_scales, uint64_t* xfer, uint32_t tag,
+                      uint32_t d_model, uint32_t d_inner, uint32_t d_state, uint32_t n_groups,
+                      uint32_t n_heads, uint32_t d_head, uint32_t d_conv, float eps,
+                      lssm_wfmt wfmt, lssm_dtype act);
+
 /* hidden[i, :] = table[ids[i], :]  (Mamba2Model::embed, mamba2_model.cpp:128-137). */
 int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out,
                uint32_t n, uint32_t d_model, uint32_t vocab, lssm_dtype act);
@@ -362,10 +385,12 @@ int lssm_engine_logits(lssm_engine* e, void** logits);          /* [max_batch, v
 int lssm_engine_state(lssm_engine* e, void** conv_state, void** ssd_state);
 /* conv_state: [n_layer, max_batch, xBC_dim, d_conv] act; ssd: [n_layer, max_batch, H, P, N] f32 */
 /* Layers of the last decode step (eager or captured) whose SSD step ran inside
- * the in_proj launch (batch 1; the environment variable LSSM_FUSED_SSD=0 at
- * engine creation turns that off).  No counterpart in the reference, whose
- * decode runs every op as its own kernel. */
-int lssm_engine_fused_layers(lssm_engine* e, uint32_t* layers);
+ * the in_proj launch (ssd_fused), and of those, layers whose whole mixer
+ * (in_proj .. SSD step .. out_proj + residual) ran as one launch (mixer_fused).
+ * Batch 1 only; the environment variable LSSM_FUSED_SSD=0 at engine creation
+ * turns both off.  Either pointer may be null.  No counterpart in the
+ * reference, whose decode runs every op as its own kernel. */
+int lssm_engine_fused_layers(lssm_engine* e, uint32_t* ssd_fused, uint32_t* mixer_fused);
 
 #ifdef __cplusplus
 }

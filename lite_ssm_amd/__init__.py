@@ -142,6 +142,7 @@ _SIGS = {
     "lssm_ssd_step": ([_vp] + [_vp] * 9 + [_u32, SSDStepDims, _i], _i),
     "lssm_inproj_decode": ([_vp] * 11 + [_u32] * 7 + [_f, _i, _i], _i),
     "lssm_inproj_ssd_decode": ([_vp] * 14 + [_u32] * 8 + [_f, _i, _i], _i),
+    "lssm_mixer_decode": ([_vp] * 16 + [_u32] * 8 + [_f, _i, _i], _i),
     "lssm_embed": ([_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i], _i),
     "lssm_argmax": ([_vp, _vp, _vp, _u32, _u32, _i], _i),
     # engine
@@ -154,7 +155,7 @@ _SIGS = {
     "lssm_engine_decode_graph": ([_vp, _vp, _u32, _vp, _u32], _i),
     "lssm_engine_logits": ([_vp, C.POINTER(_vp)], _i),
     "lssm_engine_state": ([_vp, C.POINTER(_vp), C.POINTER(_vp)], _i),
-    "lssm_engine_fused_layers": ([_vp, C.POINTER(C.c_uint32)], _i),
+    "lssm_engine_fused_layers": ([_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)], _i),
 }
 
 

@@ -321,6 +321,46 @@ int lssm_inproj_ssd_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w
     return finish(ctx, "inproj_ssd_decode");
 }
 
+int lssm_mixer_decode(lssm_ctx* ctx, void* hidden, const void* norm_w, const void* in_w,
+                      const void* in_scales, void* conv_state, const void* conv_w,
+                      const void* conv_b, const void* dt_bias, const void* A_log,
+                      const void* D_skip, float* ssd_state, const void* mixer_norm_w,
+                      const void* out_w, const void* out_scales, uint64_t* xfer, uint32_t tag,
+                      uint32_t d_model, uint32_t d_inner, uint32_t d_state, uint32_t n_groups,
+                      uint32_t n_heads, uint32_t d_head, uint32_t d_conv, float eps,
+                      lssm_wfmt wfmt, lssm_dtype act) {
+    LSSM_CHECK_CTX(ctx);
+    LSSM_REQUIRE(valid_act(act), "mixer_decode: unknown dtype");
+    if (int rc = check_fmt_k(d_model, wfmt, in_scales)) return rc;
+    if (int rc = check_fmt_k(d_inner, wfmt, out_scales)) return rc;
+    LSSM_REQUIRE(hidden && xfer && ssd_state && norm_w && mixer_norm_w && A_log && dt_bias && out_w,
+                 "mixer_decode: null pointer");
+    LSSM_REQUIRE(n_heads >= 1 && n_groups >= 1 && d_inner == n_heads * d_head,
+                 "mixer_decode: d_inner must equal n_heads * d_head");
+    const uint32_t xbc = d_inner + 2u * n_groups * d_state, proj = d_inner + xbc + n_heads;
+    InprojDecodeArgs a;
+    a.g = GemvArgs{hidden, d_model, in_w, in_scales, nullptr, 0, nullptr, norm_w, eps, 1u, proj, d_model,
+                   wfmt, act, LSSM_EPI_NONE};
+    a.d_inner = d_inner;
+    a.xbc = xbc;
+    a.H = n_heads;
+    a.dconv = d_conv;
+    a.conv_state = conv_state;
+    a.conv_w = conv_w;
+    a.conv_b = conv_b;
+    a.z = nullptr;
+    a.xbc_act = nullptr;
+    a.dt = nullptr;
+    const SsdFuseArgs f{xfer, nullptr, tag, ssd_state, A_log, dt_bias, D_skip, nullptr, d_head, d_state, n_groups,
+                        1e-6f, 1e6f};
+    const OutprojFuseArgs o{out_w, out_scales, mixer_norm_w, eps, hidden, reinterpret_cast<uint32_t*>(xfer + proj), d_model};
+    hipError_t e = hipSuccess;
+    if (!launch_layer_decode(ctx->stream, a, f, o, e))
+        return set_error(LSSM_EINVAL, "mixer_decode: shape, format, alignment or grid not supported by the fused launch");
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "mixer_decode: %s", hipGetErrorString(e));
+    return finish(ctx, "mixer_decode");
+}
+
 int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out, uint32_t n,
                uint32_t d_model, uint32_t vocab, lssm_dtype act) {
     LSSM_CHECK_CTX(ctx);

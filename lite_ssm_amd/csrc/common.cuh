@@ -28,6 +28,15 @@ __device__ __forceinline__ float to_f(bf16 v) { return (float)v; }
 __device__ __forceinline__ float to_f(float v) { return v; }
 
 template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v; }
+// fp32 -> fp16 rounds the fp32 value as it stands (the reference computes in
+// float and converts to half).  The empty asm keeps the compiler from folding
+// the conversion into the multiply or FMA that produced v: the mixed-precision
+// FMA it would use rounds the exact result straight to fp16, which differs in
+// rare ties from rounding to fp32 first.
+template <> __device__ __forceinline__ f16 from_f<f16>(float v) {
+    asm("" : "+v"(v));
+    return (f16)v;
+}
 
 // r(): round to the storage type and back.
 template <typename T> __device__ __forceinline__ float rnd(float v) { return to_f(from_f<T>(v)); }

@@ -60,14 +60,22 @@ struct lssm_engine {
     void* conv_state = nullptr;
     float* ssd_state = nullptr;
     void* argmax_scratch = nullptr;
-    // batch-1 decode: in_proj and the SSD step in one launch (tagged words of
-    // each layer's projection; the tag is a step counter the embedding
-    // advances).  Both are zeroed once at creation and never reset together
-    // with a live tag.  LSSM_FUSED_SSD=0 in the environment turns it off.
+    // batch-1 decode: in_proj, the SSD step (and out_proj) in one launch
+    // (tagged words of each layer's projection and gated SSD output; the tag
+    // is a count of batch-1 steps the embedding advances, so consecutive uses
+    // of a layer's words differ by one).  Both are zeroed once at creation
+    // and never reset apart.  LSSM_FUSED_SSD=0 in the environment turns it off.
     uint64_t* xfer = nullptr;
     uint32_t* seq = nullptr;
     bool fuse_ssd = true;
-    mutable uint32_t fused_layers = 0;   // of the last decode step issued
+    // LSSM_FUSED_MIXER=1: out_proj in the same launch too (bit-identical; on
+    // the 2.7B shape it measures ~3 % slower than a separate out_proj launch:
+    // its two waits on other workgroups' words cost more than one kernel
+    // boundary), so it is off by default
+    bool fuse_mixer = false;
+    mutable uint32_t fused_layers = 0;   // of the last decode step issued: SSD in the in_proj launch
+    mutable uint32_t mixer_layers = 0;   //   the whole mixer (+ out_proj) in one launch
+    size_t xfer_words() const { return (size_t)proj + d_inner; }   // per layer: [z|xBC|dt] + gated y
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -130,7 +138,10 @@ struct lssm_engine {
 
     // One decode step: ids -> next (all on device).  mamba2_block.cpp:317-327.
     hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
-        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act, fuse_ssd ? seq : nullptr);
+        // the step tag advances on batch-1 steps only, the ones that use the
+        // tagged words: every use then finds the previous use's tag, minus one
+        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act,
+                                    fuse_ssd && B == 1 ? seq : nullptr);
         // fused RMSNorm + linear kernels: the VALU GEMV up to 4 rows, the MFMA
         // GEMV for decode batches of the shapes it takes
         const bool fused_in = (B <= 4 && (int)B <= gemv_max_rows(d_model, wfmt, act)) ||
@@ -138,10 +149,12 @@ struct lssm_engine {
         const bool fused_out = (B <= 4 && gemv_max_rows(d_inner, wfmt, act) >= 1) ||
                                (B >= 2 && gemv_mma_takes(B, d_model, d_inner, wfmt, act));
         fused_layers = 0;
+        mixer_layers = 0;
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
             char* cs = conv_layer(li);
             bool ssd_done = false;   // the SSD step ran inside the in_proj launch
+            bool out_done = false;   //   and out_proj too
             if (fused_in) {
                 InprojDecodeArgs a;
                 a.g = GemvArgs{d_hidden, d_model, w.in_proj_w, w.in_proj_s, nullptr, 0, nullptr,
@@ -157,10 +170,17 @@ struct lssm_engine {
                 a.xbc_act = d_xbc;
                 a.dt = d_dt;
                 if (B == 1 && fuse_ssd) {
-                    const SsdFuseArgs f{xfer + (size_t)li * proj, seq, 0u, ssd_layer(li), w.A_log, w.dt_bias, w.D,
+                    uint64_t* lx = xfer + (size_t)li * xfer_words();
+                    const SsdFuseArgs f{lx, seq, 0u, ssd_layer(li), w.A_log, w.dt_bias, w.D,
                                         d_g, P, N, G, DT_MIN, DT_MAX};
-                    ssd_done = launch_inproj_ssd_decode(st(), a, f, e);
+                    if (fused_out && fuse_mixer) {
+                        const OutprojFuseArgs o{w.out_proj_w, w.out_proj_s, w.mixer_norm_w, RMS_EPS, d_hidden,
+                                                reinterpret_cast<uint32_t*>(lx + proj), d_model};
+                        out_done = ssd_done = launch_layer_decode(st(), a, f, o, e);
+                    }
+                    if (!ssd_done) ssd_done = launch_inproj_ssd_decode(st(), a, f, e);
                     fused_layers += ssd_done ? 1u : 0u;
+                    mixer_layers += out_done ? 1u : 0u;
                 }
                 if (!ssd_done) e = launch_inproj_decode(st(), a);
             } else {
@@ -185,6 +205,7 @@ struct lssm_engine {
                       z, zs};
             if (!ssd_done) e = launch_ssd_step(st(), s);
             if (e != hipSuccess) break;
+            if (out_done) continue;
             if (fused_out) {
                 GemvArgs g{d_g, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden,
                            w.mixer_norm_w, RMS_EPS, B, d_model, d_inner, wfmt, act, LSSM_EPI_ADD};
@@ -373,7 +394,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A(&e->conv_state, (size_t)cfg->n_layer * max_batch * e->xbc * e->K * es);
     A((void**)&e->ssd_state, (size_t)cfg->n_layer * max_batch * e->H * e->P * e->N * sizeof(float));
     A(&e->argmax_scratch, (size_t)max_batch * 128 * 8);
-    const size_t xfer_bytes = (size_t)cfg->n_layer * e->proj * sizeof(uint64_t);
+    const size_t xfer_bytes = (size_t)cfg->n_layer * e->xfer_words() * sizeof(uint64_t);
     A((void**)&e->xfer, xfer_bytes);
     A((void**)&e->seq, 256);
     if (rc == LSSM_OK) {
@@ -382,6 +403,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
         if (err != hipSuccess) rc = set_error(LSSM_EDEVICE, "engine_create: %s", hipGetErrorString(err));
     }
     if (const char* v = getenv("LSSM_FUSED_SSD")) e->fuse_ssd = v[0] != '0';
+    if (const char* v = getenv("LSSM_FUSED_MIXER")) e->fuse_mixer = v[0] == '1';
     if (rc != LSSM_OK) {
         delete e;
         return rc;
@@ -468,10 +490,10 @@ int lssm_engine_logits(lssm_engine* e, void** logits) {
     return LSSM_OK;
 }
 
-int lssm_engine_fused_layers(lssm_engine* e, uint32_t* layers) {
+int lssm_engine_fused_layers(lssm_engine* e, uint32_t* ssd_fused, uint32_t* mixer_fused) {
     if (int rc = check_engine(e)) return rc;
-    LSSM_REQUIRE(layers, "engine_fused_layers: null out");
-    *layers = e->fused_layers;
+    if (ssd_fused) *ssd_fused = e->fused_layers;
+    if (mixer_fused) *mixer_fused = e->mixer_layers;
     return LSSM_OK;
 }
 

@@ -244,7 +244,7 @@ template <typename T> __device__ __forceinline__ uint32_t pk2(float lo, float hi
         return __builtin_bit_cast(uint32_t, v2{(__bf16)lo, (__bf16)hi});
     } else {
         typedef _Float16 v2 __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(uint32_t, v2{(_Float16)lo, (_Float16)hi});
+        return __builtin_bit_cast(uint32_t, v2{from_f<f16>(lo), from_f<f16>(hi)});
     }
 }
 

@@ -29,6 +29,8 @@
 //  * gemv_lds (any dtype, any alignment): x rows staged once per block in LDS
 //    as fp32, padded by 4 floats per chunk so that the 16-byte reads of the 16
 //    lanes of a row fall in distinct banks; 16 lanes per row.
+#include <type_traits>
+
 #include "gemv_core.cuh"
 
 namespace lssm {
@@ -70,7 +72,9 @@ template <typename T> struct EpiInprojSsd {
     const T* A_log;
     const T* dt_bias;
     const T* D;                                           // nullptr: no D term
-    T* y;                                                 // [d_inner] gated SSD output
+    T* y;                                                 // [d_inner] gated SSD output, or
+    uint32_t* yx;                                         //   tagged 32-bit words when set:
+                                                          //   value | (tag mod 2^16) << 16
     uint32_t P, G, items;                                 // items = H * P / IP
     float dt_min, dt_max;
     using Pre = typename EpiInproj<T>::Pre;
@@ -78,6 +82,7 @@ template <typename T> struct EpiInprojSsd {
         f32x4 s[F];
         uint32_t alr, dbr, dr;
     };
+    bool fits(uint32_t) const { return true; }           // host: workgroup size check
     __device__ __forceinline__ void pin() const {
         in.pin();
         pin_arg(xfer);
@@ -99,8 +104,7 @@ template <typename T> struct EpiInprojSsd {
     // The state columns and head scalars of the block's first item, requested
     // right behind the weights (every thread loads: clamped, values unused
     // where there is no item).
-    __device__ __forceinline__ Early early() const {
-        Early e;
+    __device__ __forceinline__ void early(Early& e) const {
         const uint32_t it = blockIdx.x < items ? blockIdx.x : items - 1;
         const uint32_t t = threadIdx.x % (IP * NV);
         const uint32_t ipp = P / IP, h = it / ipp, p = (it % ipp) * IP + t / NV;
@@ -110,74 +114,321 @@ template <typename T> struct EpiInprojSsd {
         e.alr = raw_at(A_log + h);
         e.dbr = raw_at(dt_bias + h);
         e.dr = raw_at(D ? D + h : A_log + h);             // value unused without D
-        return e;
     }
-    __device__ __forceinline__ void tail(const Early& e) const {
+    // One (head, 32-column) item: wait for its words, then the SSD step + gate.
+    __device__ __forceinline__ void item(uint32_t it, const f32x4 (&s)[F], uint32_t alr, uint32_t dbr, uint32_t dr,
+                                         uint32_t tag) const {
         __shared__ uint32_t wv[NWD];                      // B, C, x, z, dt value bits
         constexpr uint32_t QNAN = __is_same(T, f16) ? 0x7E00u : 0x7FC0u;
-        const uint32_t tag = seq ? *seq : tag0;
         const uint32_t d_inner = in.d_inner, H = in.H, GN = G * NN, ipp = P / IP;
-        for (uint32_t it = blockIdx.x; it < items; it += gridDim.x) {
-            const uint32_t h = it / ipp, p0 = (it % ipp) * IP, g = h / (H / G);
-            __syncthreads();                              // the previous item's words read
-            for (uint32_t t = threadIdx.x; t < NWD; t += blockDim.x) {
-                uint32_t idx;
-                if (t < NN) idx = 2 * d_inner + g * NN + t;                              // B
-                else if (t < 2 * NN) idx = 2 * d_inner + GN + g * NN + (t - NN);         // C
-                else if (t < 2 * NN + IP) idx = d_inner + h * P + p0 + (t - 2 * NN);     // x
-                else if (t < 2 * NN + 2 * IP) idx = h * P + p0 + (t - 2 * NN - IP);      // z
-                else idx = d_inner + in.xbc + h;                                         // dt
-                uint64_t v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                for (uint32_t n = 0; (uint32_t)(v >> 32) != tag && n < SPIN; ++n)
-                    v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                wv[t] = (uint32_t)(v >> 32) == tag ? (uint32_t)v : QNAN;
+        const uint32_t h = it / ipp, p0 = (it % ipp) * IP, g = h / (H / G);
+        __syncthreads();                                  // a previous item's words read
+        for (uint32_t t = threadIdx.x; t < NWD; t += blockDim.x) {
+            uint32_t idx;
+            if (t < NN) idx = 2 * d_inner + g * NN + t;                              // B
+            else if (t < 2 * NN) idx = 2 * d_inner + GN + g * NN + (t - NN);         // C
+            else if (t < 2 * NN + IP) idx = d_inner + h * P + p0 + (t - 2 * NN);     // x
+            else if (t < 2 * NN + 2 * IP) idx = h * P + p0 + (t - 2 * NN - IP);      // z
+            else idx = d_inner + in.xbc + h;                                         // dt
+            uint64_t v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t n = 0; (uint32_t)(v >> 32) != tag && n < SPIN; ++n)
+                v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wv[t] = (uint32_t)(v >> 32) == tag ? (uint32_t)v : QNAN;
+        }
+        __syncthreads();
+        if (threadIdx.x >= IP * NV) return;               // wave-uniform; no barrier follows
+        const uint32_t lr = threadIdx.x % NV, pl = threadIdx.x / NV;
+        f32x4* S = reinterpret_cast<f32x4*>(state + ((size_t)h * P + p0 + pl) * NN);
+        const float xv = f_of_raw<T>(wv[2 * NN + pl]);
+        const float A_h = -expf(f_of_raw<T>(alr));
+        float dt = softplus_f(f_of_raw<T>(wv[2 * NN + 2 * IP]) + f_of_raw<T>(dbr));
+        dt = fminf(fmaxf(dt, dt_min), dt_max);
+        const float decay = expf(A_h * dt);
+        float ys = 0.0f;
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+            const uint32_t n0 = 4 * (lr + NV * f);
+            const float b0 = f_of_raw<T>(wv[n0]), b1 = f_of_raw<T>(wv[n0 + 1]);
+            const float b2 = f_of_raw<T>(wv[n0 + 2]), b3 = f_of_raw<T>(wv[n0 + 3]);
+            const float c0 = f_of_raw<T>(wv[NN + n0]), c1 = f_of_raw<T>(wv[NN + n0 + 1]);
+            const float c2 = f_of_raw<T>(wv[NN + n0 + 2]), c3 = f_of_raw<T>(wv[NN + n0 + 3]);
+            // the same fused multiply-adds as ssd_step_kernel
+            f32x4 t = s[f];
+            t.x = fmaf(decay, t.x, dt * b0 * xv);
+            t.y = fmaf(decay, t.y, dt * b1 * xv);
+            t.z = fmaf(decay, t.z, dt * b2 * xv);
+            t.w = fmaf(decay, t.w, dt * b3 * xv);
+            S[lr + NV * f] = t;
+            ys += fmaf(c3, t.w, fmaf(c2, t.z, fmaf(c0, t.x, c1 * t.y)));
+        }
+        ys = group_sum<NV>(ys);
+        if (lr == 0) {
+            float yv = rnd<T>(fmaf(D ? f_of_raw<T>(dr) : 0.0f, xv, ys));
+            yv = silu_fast(f_of_raw<T>(wv[2 * NN + IP + pl])) * yv;
+            const size_t yi = (size_t)h * P + p0 + pl;
+            if (yx) __hip_atomic_store(yx + yi, bits16(from_f<T>(yv)) | (tag << 16), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            else y[yi] = from_f<T>(yv);
+        }
+    }
+    __device__ __forceinline__ void tail(const Early& e) const {
+        const uint32_t tag = seq ? *seq : tag0;
+        if (blockIdx.x < items) item(blockIdx.x, e.s, e.alr, e.dbr, e.dr, tag);
+        // items beyond one per workgroup (not with the engine's shapes): state loaded here
+        const uint32_t ipp = P / IP;
+        for (uint32_t it = blockIdx.x + gridDim.x; it < items; it += gridDim.x) {
+            const uint32_t h = it / ipp, p = (it % ipp) * IP + threadIdx.x % (IP * NV) / NV;
+            const f32x4* S = reinterpret_cast<const f32x4*>(state + ((size_t)h * P + p) * NN);
+            f32x4 s[F];
+#pragma unroll
+            for (int f = 0; f < F; ++f) s[f] = S[threadIdx.x % NV + NV * f];
+            item(it, s, raw_at(A_log + h), raw_at(dt_bias + h), raw_at(D ? D + h : A_log + h), tag);
+        }
+    }
+};
+
+// Engine decode at batch 1, a layer's whole mixer in one launch: EpiInprojSsd
+// with the gated SSD outputs published as tagged words too, then out_proj with
+// its gated-RMSNorm prologue and residual add, over weights requested behind
+// the in_proj weights and held in registers.  Every workgroup waits for all
+// d_inner words and stages them exactly as the separate out_proj launch
+// (gemv1_kernel, NORM) would with its own workgroup size BDV: threads below
+// BDV take the octets that launch's threads take, in the same order, so the
+// sum of squares, the staged pairs and every row come out bit-identical.
+// Row group r of out_proj goes to wave r % W of workgroup r / W (W waves per
+// workgroup), so that only the first workgroups wait for the gated outputs.
+// `hid` is read by every workgroup's in_proj staging and rewritten by the
+// out_proj rows; a row is written only once all gated outputs exist, i.e.
+// after every workgroup has staged and published its in_proj rows.
+template <typename T, int FMT, int LPR2, int CPL2> struct EpiLayer {
+    using S = EpiInprojSsd<T>;
+    using F = Fmt<FMT, T>;
+    static constexpr bool kNormOptional = false;
+    static constexpr bool kTail = true;
+    static constexpr int WPC = F::WPC, NP = WPC / 2, XS = xs_of<NP>();
+    static constexpr int RPW2 = WAVE / LPR2;
+    static constexpr uint32_t K2 = (uint32_t)LPR2 * CPL2 * WPC;   // the d_inner this is built for
+    static constexpr uint32_t CPR2 = K2 / WPC, NOCT2 = K2 / 8;
+    static constexpr int OCT2 = (int)((NOCT2 + G1_NT - 1) / G1_NT);
+    static constexpr bool BIAS = q4_bf16<FMT, T>();
+    static constexpr uint32_t GD = F::G ? F::G : 1;
+    S ssd;                       // in_proj epilogue + SSD items, ssd.yx set
+    const uint8_t* w2;           // out_proj [d_model, d_inner]
+    const uint16_t* s2;
+    const T* nw2;                // mixer (gated) norm weight [d_inner]
+    float eps2;
+    T* hid;                      // [d_model]: residual in, hidden out
+    uint32_t N2;                 // d_model
+    uint32_t bdv;                // the separate out_proj launch's workgroup size
+    using Pre = typename S::Pre;
+    // host: the staging above needs bdv's whole waves inside this launch's workgroups
+    bool fits(uint32_t bd) const { return bdv % WAVE == 0 && bdv <= bd && bdv / WAVE <= 16; }
+    struct Early {                                       // (vector types: a struct uint4
+        typename S::Early e;                             //  would copy through scratch)
+        u32x4 wq[CPL2];
+        uint16_t sc[CPL2];
+        uint32_t res;
+        u32x4 nw[OCT2];
+    };
+    __device__ __forceinline__ void pin() const {
+        ssd.pin();
+        pin_arg(w2);
+        pin_arg(s2);
+        pin_arg(nw2);
+        pin_arg(hid);
+        pin_arg(N2);
+        pin_arg(bdv);
+    }
+    __device__ __forceinline__ Pre prefetch(int m, uint32_t n) const { return ssd.prefetch(m, n); }
+    __device__ __forceinline__ void operator()(int m, uint32_t n, float acc, const Pre& p) const {
+        ssd(m, n, acc, p);
+    }
+    // this workgroup's out_proj rows: weights, scales, residual; the norm
+    // weight octets its threads below bdv stage
+    __device__ __forceinline__ void early(Early& e) const {
+        ssd.early(e.e);
+        const uint32_t ng = (N2 + RPW2 - 1) / RPW2;
+        const uint32_t rg = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+        uint32_t n = (rg < ng ? rg : ng - 1) * RPW2 + (threadIdx.x % WAVE) / LPR2;
+        n = n < N2 ? n : N2 - 1;                        // clamped: every lane loads
+        const uint32_t lr = threadIdx.x % LPR2;
+        const uint8_t* wr = w2 + (size_t)n * F::row_bytes(K2);
+#pragma unroll
+        for (int j = 0; j < CPL2; ++j) {
+            e.wq[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (size_t)(lr + LPR2 * j) * 16));
+        }
+        if constexpr (F::G > 0) {
+#pragma unroll
+            for (int j = 0; j < CPL2; ++j) e.sc[j] = s2[(size_t)n * (K2 / GD) + ((lr + LPR2 * j) * WPC) / GD];
+        }
+        e.res = raw_at(hid + n);
+#pragma unroll
+        for (int i = 0; i < OCT2; ++i) {
+            uint32_t o = threadIdx.x + bdv * i;
+            o = o < NOCT2 ? o : NOCT2 - 1;
+            e.nw[i] = reinterpret_cast<const u32x4*>(nw2)[o];
+        }
+    }
+    __device__ __forceinline__ void tail(const Early& e) const {
+        __shared__ uint32_t xl2[CPR2 * XS];
+        __shared__ float red2[16];
+        ssd.tail(e.e);
+        const uint32_t tag = ssd.seq ? *ssd.seq : ssd.tag0;
+        constexpr uint32_t QNAN = __is_same(T, f16) ? 0x7E00u : 0x7FC0u;
+        const int lane = threadIdx.x % WAVE;
+        const uint32_t wbase = threadIdx.x & ~(uint32_t)(WAVE - 1);
+        // ---- the gated outputs, as octets of packed pairs (threads < bdv) ----
+        // Only the workgroups with out_proj rows wait for the gated outputs;
+        // each reads the d_inner 32-bit words coalesced (a lane a word, all
+        // of a lane's words requested at once, stale ones asked for again)
+        // into LDS, from where the threads below bdv pick up their octets.
+        const uint32_t nwb = blockDim.x / WAVE;
+        const uint32_t ng = (N2 + RPW2 - 1) / RPW2;
+        if (blockIdx.x * nwb >= ng) return;              // workgroup-uniform; no barrier follows
+        __shared__ __attribute__((aligned(16))) uint16_t ybuf[K2];
+        const uint32_t tag16 = tag & 0xFFFFu;
+        for (uint32_t k0 = 0; k0 < K2; k0 += 8 * blockDim.x) {   // rounds of 8 words a lane
+            uint32_t x[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                uint32_t k = k0 + threadIdx.x + blockDim.x * r;
+                k = k < K2 ? k : K2 - 1;                 // clamped: every lane loads
+                x[r] = __hip_atomic_load(ssd.yx + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            __syncthreads();
-            if (threadIdx.x < IP * NV) {                  // wave-uniform
-                const uint32_t lr = threadIdx.x % NV, pl = threadIdx.x / NV;
-                f32x4* S = reinterpret_cast<f32x4*>(state + ((size_t)h * P + p0 + pl) * NN);
-                f32x4 s[F];
-                uint32_t alr = e.alr, dbr = e.dbr, dr = e.dr;
-                if (it == blockIdx.x) {
+            for (uint32_t it = 0; it < S::SPIN; ++it) {
+                bool stale = false;
 #pragma unroll
-                    for (int f = 0; f < F; ++f) s[f] = e.s[f];
+                for (int r = 0; r < 8; ++r) stale |= (x[r] >> 16) != tag16;
+                if (!stale) break;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    uint32_t k = k0 + threadIdx.x + blockDim.x * r;
+                    k = k < K2 ? k : K2 - 1;
+                    if ((x[r] >> 16) != tag16)
+                        x[r] = __hip_atomic_load(ssd.yx + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const uint32_t k = k0 + threadIdx.x + blockDim.x * r;
+                if (k < K2) ybuf[k] = (uint16_t)((x[r] >> 16) == tag16 ? (x[r] & 0xFFFFu) : QNAN);
+            }
+        }
+        __syncthreads();
+        uint4 xo[OCT2];
+        if (threadIdx.x < bdv) {                         // wave-uniform (bdv: whole waves)
+#pragma unroll
+            for (int i = 0; i < OCT2; ++i) {
+                if (wbase + bdv * i >= NOCT2) break;
+                uint32_t o = threadIdx.x + bdv * i;
+                o = o < NOCT2 ? o : NOCT2 - 1;
+                xo[i] = *reinterpret_cast<const uint4*>(ybuf + 8 * o);
+            }
+        }
+        // ---- sum of squares and 1/rms, as gemv1_kernel with bdv threads ----
+        float ss = 0.0f;
+        if (threadIdx.x < bdv) {
+#pragma unroll
+            for (int i = 0; i < OCT2; ++i) {
+                if (wbase + bdv * i >= NOCT2) break;
+                const bool live = threadIdx.x + bdv * i < NOCT2;
+                const uint4 d = xo[i];
+                float q = dot2(d.x, d.x, 0.0f, T{});
+                q = dot2(d.y, d.y, q, T{});
+                q = dot2(d.z, d.z, q, T{});
+                q = dot2(d.w, d.w, q, T{});
+                ss += live ? q : 0.0f;
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0 && threadIdx.x < bdv) red2[threadIdx.x / WAVE] = ss;
+        __syncthreads();
+        float t = 0.0f;
+        for (uint32_t w = 0; w < bdv / WAVE; ++w) t += red2[w];
+        const float rr = rsqrtf(fmaf(t, 1.0f / (float)K2, eps2));   // as gemv1_kernel
+        // ---- stage r(y * w * rr) as packed pairs (+ chunk sums), as gemv1 ----
+        if (threadIdx.x < bdv) {
+            constexpr uint32_t ONES = __is_same(T, f16) ? 0x3C003C00u : 0x3F803F80u;
+#pragma unroll
+            for (int i = 0; i < OCT2; ++i) {
+                if (wbase + bdv * i >= NOCT2) break;
+                const uint32_t o = threadIdx.x + bdv * i;
+                const uint32_t k0 = o * 8, ch = k0 / WPC, off = k0 % WPC;
+                const uint32_t xd[4] = {xo[i].x, xo[i].y, xo[i].z, xo[i].w};
+                const uint32_t wd[4] = {e.nw[i][0], e.nw[i][1], e.nw[i][2], e.nw[i][3]};
+                float v[8];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[2 * q] = dot2(xd[q], wd[q] & 0x0000FFFFu, 0.0f, T{}) * rr;
+                    v[2 * q + 1] = dot2(xd[q], wd[q] & 0xFFFF0000u, 0.0f, T{}) * rr;
+                }
+                // the octet's offset in its chunk as a constant (a runtime
+                // index into v would put it in scratch)
+                uint32_t pq[4];
+                auto pairs = [&](auto offc) {
+                    constexpr int OFF = decltype(offc)::value;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        int a, b;
+                        pair_pos<FMT, T>(OFF / 2 + q, a, b);
+                        pq[q] = pack2<T>(v[a - OFF], v[b - OFF]);
+                    }
+                };
+                if constexpr (WPC == 32) {
+                    switch (off) {
+                        case 0: pairs(std::integral_constant<int, 0>{}); break;
+                        case 8: pairs(std::integral_constant<int, 8>{}); break;
+                        case 16: pairs(std::integral_constant<int, 16>{}); break;
+                        default: pairs(std::integral_constant<int, 24>{}); break;
+                    }
+                } else if constexpr (WPC == 16) {
+                    if (off == 0) pairs(std::integral_constant<int, 0>{});
+                    else pairs(std::integral_constant<int, 8>{});
                 } else {
-#pragma unroll
-                    for (int f = 0; f < F; ++f) s[f] = S[lr + NV * f];
-                    alr = raw_at(A_log + h);
-                    dbr = raw_at(dt_bias + h);
-                    dr = raw_at(D ? D + h : A_log + h);
+                    pairs(std::integral_constant<int, 0>{});   // dense: one octet per chunk
                 }
-                const float xv = f_of_raw<T>(wv[2 * NN + pl]);
-                const float A_h = -expf(f_of_raw<T>(alr));
-                float dt = softplus_f(f_of_raw<T>(wv[2 * NN + 2 * IP]) + f_of_raw<T>(dbr));
-                dt = fminf(fmaxf(dt, dt_min), dt_max);
-                const float decay = expf(A_h * dt);
-                float ys = 0.0f;
-#pragma unroll
-                for (int f = 0; f < F; ++f) {
-                    const uint32_t n0 = 4 * (lr + NV * f);
-                    const float b0 = f_of_raw<T>(wv[n0]), b1 = f_of_raw<T>(wv[n0 + 1]);
-                    const float b2 = f_of_raw<T>(wv[n0 + 2]), b3 = f_of_raw<T>(wv[n0 + 3]);
-                    const float c0 = f_of_raw<T>(wv[NN + n0]), c1 = f_of_raw<T>(wv[NN + n0 + 1]);
-                    const float c2 = f_of_raw<T>(wv[NN + n0 + 2]), c3 = f_of_raw<T>(wv[NN + n0 + 3]);
-                    // the same fused multiply-adds as ssd_step_kernel
-                    f32x4 t = s[f];
-                    t.x = fmaf(decay, t.x, dt * b0 * xv);
-                    t.y = fmaf(decay, t.y, dt * b1 * xv);
-                    t.z = fmaf(decay, t.z, dt * b2 * xv);
-                    t.w = fmaf(decay, t.w, dt * b3 * xv);
-                    S[lr + NV * f] = t;
-                    ys += fmaf(c3, t.w, fmaf(c2, t.z, fmaf(c0, t.x, c1 * t.y)));
-                }
-                ys = group_sum<NV>(ys);
-                if (lr == 0) {
-                    float yv = rnd<T>(fmaf(D ? f_of_raw<T>(dr) : 0.0f, xv, ys));
-                    yv = silu_fast(f_of_raw<T>(wv[2 * NN + IP + pl])) * yv;
-                    y[(size_t)h * P + p0 + pl] = from_f<T>(yv);
+                uint32_t* dst = xl2 + ch * XS;
+                if (o < NOCT2) *reinterpret_cast<uint4*>(dst + off / 2) = make_uint4(pq[0], pq[1], pq[2], pq[3]);
+                if constexpr (BIAS) {
+                    float sx = dot2(pq[0], ONES, 0.0f, T{});
+                    sx = dot2(pq[1], ONES, sx, T{});
+                    sx = dot2(pq[2], ONES, sx, T{});
+                    sx = dot2(pq[3], ONES, sx, T{});
+                    sx = group_sum<WPC / 8>(sx);
+                    if (o < NOCT2 && (o % (WPC / 8)) == 0) dst[NP] = __float_as_uint(sx);
                 }
             }
         }
+        __syncthreads();
+        // ---- this wave's out_proj rows (gemv1_kernel's per-row arithmetic) ----
+        const uint32_t rg = blockIdx.x * nwb + threadIdx.x / WAVE;
+        if (rg >= ng) return;                            // wave-uniform; no barrier follows
+        const uint32_t n = rg * RPW2 + lane / LPR2;
+        const uint32_t lr = lane % LPR2;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL2; ++j) {
+            const Unpacked<FMT, T> u = unpack<FMT, T>(make_uint4(e.wq[j][0], e.wq[j][1], e.wq[j][2], e.wq[j][3]));
+            float sc = 1.0f;
+            if constexpr (F::G > 0) sc = fp16_bits_to_f(e.sc[j]);
+            const uint32_t* src = xl2 + (lr + LPR2 * j) * XS;
+            uint32_t xp[NP];
+#pragma unroll
+            for (int q = 0; q < NP / 4; ++q) {
+                const uint4 vv = *reinterpret_cast<const uint4*>(src + 4 * q);
+                xp[4 * q] = vv.x;
+                xp[4 * q + 1] = vv.y;
+                xp[4 * q + 2] = vv.z;
+                xp[4 * q + 3] = vv.w;
+            }
+            float d = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NP; ++q) d = dot2(u.p[q], xp[q], d, T{});
+            if constexpr (BIAS) d -= 136.0f * __uint_as_float(src[NP]);
+            acc = fmaf(d, sc, acc);                     // as gemv1_kernel
+        }
+        const float a = group_sum<LPR2>(acc);
+        if (lr == 0 && n < N2) hid[n] = from_f<T>(f_of_raw<T>(e.res) + rnd<T>(a));
     }
 };
 
@@ -322,7 +573,7 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
         for (int m = 0; m < MR; ++m) {
             float t = 0.0f;
             for (uint32_t w = 0; w < NWB; ++w) t += red[m][w];
-            rr[m] = rsqrtf(t * c.inv_k + c.eps);
+            rr[m] = rsqrtf(fmaf(t, c.inv_k, c.eps));
         }
     } else {
         // no norm: the block meets once its x loads are issued (no wait)
@@ -390,8 +641,8 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
     // held for as long as the memory system pushes back, and no barrier may
     // wait on that.
     load_w(A);
-    [[maybe_unused]] typename EarlyOf<Epi>::type early{};
-    if constexpr (Epi::kTail) early = epi.early();
+    [[maybe_unused]] typename EarlyOf<Epi>::type early;
+    if constexpr (Epi::kTail) epi.early(early);
 
 
     // ---- 4. rows; the next row's loads are in flight while this one is reduced ----
@@ -420,7 +671,7 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
 #pragma unroll
                 for (int q = 0; q < NP; ++q) d = dot2(u.p[q], xp[q], d, T{});
                 if constexpr (BIAS) d -= 136.0f * __uint_as_float(src[NP]);
-                acc[m] += d * sc;
+                acc[m] = fmaf(d, sc, acc[m]);           // spelled out: the one-launch mixer matches it
             }
         }
 #pragma unroll
@@ -482,7 +733,7 @@ hipError_t go1(hipStream_t s, const GemvCore& c, const Epi& e, int mr, int norm)
     // a tail that waits on other blocks' rows needs every block resident: one
     // block per CU (up to 16 waves at <= 128 VGPRs fits an idle CU)
     if constexpr (Epi::kTail) {
-        if (blocks > num_cus() || MR != 1) return hipErrorNotSupported;
+        if (blocks > num_cus() || MR != 1 || !e.fits(wpb * WAVE)) return hipErrorNotSupported;
     }
     auto run = [&](auto k) -> hipError_t {
         // opt in to the full dynamic LDS once per instantiation (a host attribute)
@@ -845,6 +1096,29 @@ hipError_t launch_inproj_decode(hipStream_t s, const InprojDecodeArgs& a) {
     return go(float{});
 }
 
+namespace {
+template <typename T> EpiInprojSsd<T> make_ssd_epi(const InprojDecodeArgs& a, const SsdFuseArgs& f) {
+    EpiInprojSsd<T> e{};
+    e.in = EpiInproj<T>{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,
+                        (const T*)a.conv_b, nullptr, nullptr, nullptr};
+    e.xfer = f.xfer;
+    e.seq = f.seq;
+    e.tag0 = f.tag;
+    e.state = f.state;
+    e.A_log = (const T*)f.A_log;
+    e.dt_bias = (const T*)f.dt_bias;
+    e.D = (const T*)f.D;
+    e.y = (T*)f.y;
+    e.yx = nullptr;
+    e.P = f.P;
+    e.G = f.G;
+    e.items = a.H * (f.P / EpiInprojSsd<T>::IP);
+    e.dt_min = f.dt_min;
+    e.dt_max = f.dt_max;
+    return e;
+}
+}  // namespace
+
 bool launch_inproj_ssd_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseArgs& f, hipError_t& err) {
     err = hipSuccess;
     const GemvArgs& g = a.g;
@@ -861,27 +1135,76 @@ bool launch_inproj_ssd_decode(hipStream_t s, const InprojDecodeArgs& a, const Ss
     GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
     auto go = [&](auto tag) -> hipError_t {
         using T = decltype(tag);
-        EpiInprojSsd<T> e{};
-        e.in = EpiInproj<T>{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,
-                            (const T*)a.conv_b, nullptr, nullptr, nullptr};
-        e.xfer = f.xfer;
-        e.seq = f.seq;
-        e.tag0 = f.tag;
-        e.state = f.state;
-        e.A_log = (const T*)f.A_log;
-        e.dt_bias = (const T*)f.dt_bias;
-        e.D = (const T*)f.D;
-        e.y = (T*)f.y;
-        e.P = f.P;
-        e.G = f.G;
-        e.items = a.H * (f.P / EpiInprojSsd<T>::IP);
-        e.dt_min = f.dt_min;
-        e.dt_max = f.dt_max;
+        const EpiInprojSsd<T> e = make_ssd_epi<T>(a, f);
         bool done = false;
         hipError_t r = hipErrorNotSupported;
         if (g.wfmt == LSSM_W_Q4_G64) r = launch_gemv1<LSSM_W_Q4_G64, T, 1, EpiInprojSsd<T>>(s, c, e, 1, 1, done);
         else if constexpr (__is_same(T, f16)) r = launch_gemv1<LSSM_W_Q8_G32, T, 1, EpiInprojSsd<T>>(s, c, e, 1, 1, done);
         return done ? r : hipErrorNotSupported;
+    };
+    const hipError_t r = g.act == LSSM_F16 ? go(f16{}) : go(bf16{});
+    if (r == hipErrorNotSupported) return false;   // nothing launched
+    err = r;
+    return true;
+}
+
+namespace {
+// Workgroup size gemv1 picks for a single-row launch of N rows at lpr lanes
+// per row (go1's rule).
+uint32_t gemv1_bd(uint32_t N, uint32_t lpr) {
+    const uint32_t ngroups = (N + (WAVE / lpr) - 1) / (WAVE / lpr);
+    const uint32_t per_cu = (ngroups + num_cus() - 1) / num_cus();
+    const uint32_t nw = G1_NT / WAVE;
+    return WAVE * (per_cu < nw ? nw : per_cu > 16u ? 16u : per_cu);
+}
+
+template <typename T, int FMT, int LPR, int CPL, int LPR2, int CPL2>
+hipError_t go_layer(hipStream_t s, const GemvCore& c, const EpiInprojSsd<T>& es, const OutprojFuseArgs& o) {
+    using E = EpiLayer<T, FMT, LPR2, CPL2>;
+    E e{};
+    e.ssd = es;
+    e.ssd.yx = o.yx;
+    e.w2 = (const uint8_t*)o.w;
+    e.s2 = (const uint16_t*)o.s;
+    e.nw2 = (const T*)o.norm_w;
+    e.eps2 = o.eps;
+    e.hid = (T*)o.hidden;
+    e.N2 = o.N;
+    e.bdv = gemv1_bd(o.N, LPR2);
+    return go1<FMT, T, LPR, CPL, 1, E>(s, c, e, 1, 1);
+}
+}  // namespace
+
+bool launch_layer_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseArgs& f, const OutprojFuseArgs& o,
+                         hipError_t& err) {
+    err = hipSuccess;
+    const GemvArgs& g = a.g;
+    if (!o.w || !o.norm_w || !o.hidden || !o.yx || o.hidden != g.x || o.N != g.K) return false;
+    if (((uintptr_t)o.w % 16) != 0 || ((uintptr_t)o.norm_w % 16) != 0) return false;
+    if (g.wfmt != LSSM_W_DENSE && !o.s) return false;
+    // the in_proj + SSD part's own checks (launching nothing)
+    if (g.M != 1 || !g.norm_w || (g.act != LSSM_F16 && g.act != LSSM_BF16)) return false;
+    if (a.dconv != 4 || f.N != EpiInprojSsd<f16>::NN || f.P == 0 || f.P % EpiInprojSsd<f16>::IP != 0 ||
+        f.G == 0 || a.H % f.G != 0 || a.d_inner != a.H * f.P || a.xbc != a.d_inner + 2 * f.G * f.N ||
+        g.N != a.d_inner + a.xbc + a.H)
+        return false;
+    const bool aligned = ((uintptr_t)g.x % 16 == 0) && ((uintptr_t)g.norm_w % 16 == 0) &&
+                         ((uintptr_t)g.w % 16 == 0) && ((uintptr_t)f.state % 16 == 0) &&
+                         ((uintptr_t)a.conv_state % 8 == 0) && ((uintptr_t)a.conv_w % 8 == 0);
+    if (!aligned) return false;
+    GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
+    auto go = [&](auto tag) -> hipError_t {
+        using T = decltype(tag);
+        const EpiInprojSsd<T> es = make_ssd_epi<T>(a, f);
+        const uint32_t ci = g.K / wpc_of(g.wfmt, g.act), co = a.d_inner / wpc_of(g.wfmt, g.act);
+        if (g.wfmt == LSSM_W_Q4_G64) {
+            if (ci == 80 && co == 160) return go_layer<T, LSSM_W_Q4_G64, 16, 5, 32, 5>(s, c, es, o);   // 2.7B
+            if (ci == 64 && co == 64) return go_layer<T, LSSM_W_Q4_G64, 16, 4, 16, 4>(s, c, es, o);
+        } else if constexpr (__is_same(T, f16)) {
+            if (g.wfmt == LSSM_W_Q8_G32 && ci == 48 && co == 96)
+                return go_layer<T, LSSM_W_Q8_G32, 16, 3, 32, 3>(s, c, es, o);                      // 130M
+        }
+        return hipErrorNotSupported;
     };
     const hipError_t r = g.act == LSSM_F16 ? go(f16{}) : go(bf16{});
     if (r == hipErrorNotSupported) return false;   // nothing launched

@@ -191,9 +191,11 @@ template <typename T> struct EpiInproj {
                 // registers would put them in scratch)
                 auto lo = [](uint32_t d) { return f_of_raw<T>(d & 0xFFFFu); };
                 auto hi = [](uint32_t d) { return f_of_raw<T>(d >> 16); };
-                // window shift (conv1d.metal:127-130): taps 1..3 move down, x lands in 3
-                a = f_of_raw<T>(p.b) + hi(p.s.x) * lo(p.w.x) + lo(p.s.y) * hi(p.w.x) +
-                    hi(p.s.y) * lo(p.w.y) + to_f(v) * hi(p.w.y);
+                // window shift (conv1d.metal:127-130): taps 1..3 move down, x lands in 3;
+                // the multiply-adds spelled out so that every kernel using this
+                // epilogue rounds alike
+                a = fmaf(to_f(v), hi(p.w.y),
+                         fmaf(hi(p.s.y), lo(p.w.y), fmaf(lo(p.s.y), hi(p.w.x), fmaf(hi(p.s.x), lo(p.w.x), f_of_raw<T>(p.b)))));
                 uint2 ns;
                 ns.x = p.s.x >> 16 | p.s.y << 16;                                     // (s1, s2)
                 ns.y = p.s.y >> 16 | (uint32_t)__builtin_bit_cast(uint16_t, v) << 16;  // (s3, x)

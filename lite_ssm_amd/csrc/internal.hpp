@@ -192,6 +192,23 @@ struct SsdFuseArgs {
     float dt_min, dt_max;
 };
 bool launch_inproj_ssd_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseArgs& f, hipError_t& err);
+// The whole mixer of a layer at batch 1 in one launch: launch_inproj_ssd_decode
+// with the gated SSD outputs as tagged words in `yx`, then the gated-RMSNorm +
+// out_proj + residual add of the separate out_proj launch (bit-identical to
+// it), hidden rewritten in place (`hidden` must be the in_proj input).  Same
+// weight format for both projections; returns false (launching nothing) for
+// shapes it is not built for.
+struct OutprojFuseArgs {
+    const void* w;           // out_proj [N, d_inner]
+    const void* s;
+    const void* norm_w;      // mixer norm weight [d_inner]
+    float eps;
+    void* hidden;            // [N] residual in, hidden out
+    uint32_t* yx;            // [d_inner] tagged words of this layer: value | (tag mod 2^16) << 16
+    uint32_t N;              // d_model
+};
+bool launch_layer_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseArgs& f, const OutprojFuseArgs& o,
+                         hipError_t& err);
 
 // MFMA GEMV for decode batches (gemv_mma.hip): 2..64 rows, GEMV rule, RMSNorm
 // prologue when norm_w is set.  Returns false (launching nothing) when the

@@ -244,11 +244,12 @@ class Engine:
         check(lib.lssm_memcpy_d2d(self.ctx.h, out.data_ptr(), p.value, out.numel() * out.element_size()))
         return out
 
-    def fused_layers(self) -> int:
-        """Layers of the last decode step whose SSD step ran inside the in_proj launch."""
-        n = C.c_uint32()
-        check(lib.lssm_engine_fused_layers(self.h, C.byref(n)))
-        return n.value
+    def fused_layers(self):
+        """(layers of the last decode step whose SSD step ran inside the in_proj
+        launch, layers whose whole mixer ran as one launch)."""
+        a, b = C.c_uint32(), C.c_uint32()
+        check(lib.lssm_engine_fused_layers(self.h, C.byref(a), C.byref(b)))
+        return a.value, b.value
 
     def state(self):
         """(conv [n_layer, max_batch, xbc, d_conv] act, ssd [n_layer, max_batch, H, P, N] f32) copies."""

@@ -227,21 +227,51 @@ def test_engine_argument_errors(ctx):
 
 
 FUSED_CASES = [
-    ("2.7b-bf16-q4g64", "mamba2-2.7b", O.BF16, O.W_Q4_G64, dict(n_layer=2, vocab_size=512)),
-    ("130m-f16-q8g32", "mamba2-130m", O.F16, O.W_Q8_G32, dict(n_layer=2, vocab_size=1024)),
+    # tag, shape, act, wfmt, overrides, whole mixer in one launch
+    ("2.7b-bf16-q4g64", "mamba2-2.7b", O.BF16, O.W_Q4_G64, dict(n_layer=2, vocab_size=512), True),
+    ("130m-f16-q8g32", "mamba2-130m", O.F16, O.W_Q8_G32, dict(n_layer=2, vocab_size=1024), True),
+    # a (d_model, d_inner) the one-launch mixer is not built for: SSD fused only
+    ("1536-bf16-q4g64", "mamba2-130m", O.BF16, O.W_Q4_G64,
+     dict(n_layer=2, vocab_size=1024, d_model=1536, n_heads=48), False),
 ]
 
 
-@pytest.mark.parametrize("tag,name,act,wfmt,over", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
-def test_engine_fused_ssd_decode_bs1(ctx, tag, name, act, wfmt, over):
-    """Batch-1 decode with the SSD step inside the in_proj launch (tagged words
-    read across CUs): bit-identical to the three-launch decode
-    (LSSM_FUSED_SSD=0) on every step, eager and graph-replayed (the step tag
-    advances inside the graph), and within tolerance of the oracle."""
+@pytest.mark.parametrize("tag,name,act,wfmt,over,mixer", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
+def test_engine_fused_ssd_decode_bs1(ctx, tag, name, act, wfmt, over, mixer):
+    """Batch-1 decode with the SSD step (and, where built, out_proj) inside the
+    in_proj launch (tagged words read across CUs): bit-identical to the
+    three-launch decode (LSSM_FUSED_SSD=0) on every step, eager and
+    graph-replayed (the step tag advances inside the graph), and within
+    tolerance of the oracle."""
     import os
     from lite_ssm_amd.model import Engine
     L, sh, m, om = _setup(ctx, name, act, wfmt, **over)
     Lq = 40
+    os.environ["LSSM_FUSED_MIXER"] = "1"
+    try:
+        fused = Engine(ctx, m, max_batch=1, max_seq=Lq)
+    finally:
+        del os.environ["LSSM_FUSED_MIXER"]
+    os.environ["LSSM_FUSED_SSD"] = "0"
+    try:
+        plain = Engine(ctx, m, max_batch=1, max_seq=Lq)
+    finally:
+        del os.environ["LSSM_FUSED_SSD"]
+    try:
+        _fused_vs_plain(tag, sh, om, act, fused, plain, Lq, (sh.n_layer, sh.n_layer if mixer else 0))
+    finally:
+        fused.close()
+        plain.close()
+
+
+def test_engine_default_bs1_fuses_ssd_only(ctx):
+    """The default batch-1 decode runs the SSD step inside the in_proj launch
+    and out_proj as its own launch (LSSM_FUSED_MIXER unset), bit-identical to
+    the three-launch decode."""
+    import os
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-2.7b", O.BF16, O.W_Q4_G64, n_layer=2, vocab_size=512)
+    Lq = 20
     fused = Engine(ctx, m, max_batch=1, max_seq=Lq)
     os.environ["LSSM_FUSED_SSD"] = "0"
     try:
@@ -249,13 +279,13 @@ def test_engine_fused_ssd_decode_bs1(ctx, tag, name, act, wfmt, over):
     finally:
         del os.environ["LSSM_FUSED_SSD"]
     try:
-        _fused_vs_plain(tag, sh, om, act, fused, plain, Lq)
+        _fused_vs_plain("2.7b default", sh, om, O.BF16, fused, plain, Lq, (sh.n_layer, 0))
     finally:
         fused.close()
         plain.close()
 
 
-def _fused_vs_plain(tag, sh, om, act, fused, plain, Lq):
+def _fused_vs_plain(tag, sh, om, act, fused, plain, Lq, counts):
     ids = np.random.default_rng(7).integers(0, sh.vocab_size, (1, Lq)).astype(np.int32)
     n_f = torch.zeros(1, dtype=torch.int32, device="cuda")
     n_p = torch.zeros_like(n_f)
@@ -275,7 +305,7 @@ def _fused_vs_plain(tag, sh, om, act, fused, plain, Lq):
         t = torch.from_numpy(tok).cuda()
         fused.decode(t, n_f)
         plain.decode(t, n_p)
-        assert fused.fused_layers() == sh.n_layer and plain.fused_layers() == 0
+        assert fused.fused_layers() == counts and plain.fused_layers() == (0, 0)
         same(step)
         ref = om.decode(conv, ssd, tok)
         _check_logits(fused.logits(1).float().cpu().numpy(), ref, act, f"{tag} decode {step}")
@@ -285,6 +315,6 @@ def _fused_vs_plain(tag, sh, om, act, fused, plain, Lq):
     fused.decode_graph(t_f, t_f, 6)
     for _ in range(6):
         plain.decode(t_p, t_p)
-    assert fused.fused_layers() == sh.n_layer
+    assert fused.fused_layers() == counts
     assert torch.equal(t_f, t_p)
     same("graph")

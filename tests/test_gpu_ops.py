@@ -507,6 +507,55 @@ def test_inproj_ssd_decode_vs_unfused_chain(ctx, rng, d_model, d_inner, N, G, H,
         assert_close(act_host(y_f, act), ref, act, {O.F16: 2e-3, O.BF16: 1.6e-2}[act], f"y, tag {tag}")
 
 
+MIXER_CASES = [c for c in INPROJ_SSD_CASES if (c[0], c[1]) in ((2560, 5120), (768, 1536), (2048, 2048))]
+
+
+@pytest.mark.parametrize("d_model,d_inner,N,G,H,act,wfmt", MIXER_CASES,
+                         ids=[f"dm{c[0]}-h{c[4]}-g{c[3]}" for c in MIXER_CASES])
+def test_mixer_decode_vs_two_launches(ctx, rng, d_model, d_inner, N, G, H, act, wfmt):
+    """A layer's whole batch-1 mixer in one launch == lssm_inproj_ssd_decode ->
+    lssm_norm_linear_decode(EPI_ADD), bit for bit (hidden, conv and SSD state),
+    on three calls in a row (tags 1, 2, 3)."""
+    import lite_ssm_amd as L
+    P, K = d_inner // H, 4
+    xbc = d_inner + 2 * G * N
+    proj = d_inner + xbc + H
+    nw = dev(O.to_act(1 + 0.1 * rng.standard_normal(d_model), act))
+    mnw = dev(O.to_act(1 + 0.1 * rng.standard_normal(d_inner), act))
+    wi, si = _weights(rng, proj, d_model, wfmt, act)
+    wo, so = _weights(rng, d_model, d_inner, wfmt, act)
+    wi, si, wo, so = dev(wi), dev(si), dev(wo), dev(so)
+    cw = dev(O.to_act(rng.standard_normal((xbc, K)) * 0.3, act))
+    cb = dev(O.to_act(rng.standard_normal(xbc) * 0.1, act))
+    dtb = dev(O.to_act(rng.standard_normal(H) * 0.5, act))
+    alog = dev(O.to_act(rng.uniform(0, np.log(16), H), act))
+    Dh = dev(O.to_act(rng.standard_normal(H), act))
+    cs0 = O.to_act(rng.standard_normal((1, xbc, K)), act)
+    st0 = (rng.standard_normal((H, P, N)) * 0.1).astype(np.float32)
+    h0 = O.to_act(rng.standard_normal((1, d_model)) * 0.5, act)
+    cs_f, cs_u, st_f, st_u, h_f, h_u = dev(cs0), dev(cs0), dev(st0), dev(st0), dev(h0), dev(h0)
+    xf = torch.zeros(proj + d_inner, dtype=torch.int64, device="cuda")
+    xu = torch.zeros(proj, dtype=torch.int64, device="cuda")
+    yg = empty((1, d_inner), act)
+    for tag in (1, 2, 3):
+        L.check(L.lib.lssm_mixer_decode(
+            ctx.h, h_f.data_ptr(), nw.data_ptr(), wi.data_ptr(), si.data_ptr(), cs_f.data_ptr(), cw.data_ptr(),
+            cb.data_ptr(), dtb.data_ptr(), alog.data_ptr(), Dh.data_ptr(), st_f.data_ptr(), mnw.data_ptr(),
+            wo.data_ptr(), so.data_ptr(), xf.data_ptr(), tag, d_model, d_inner, N, G, H, P, K, 1e-5, wfmt, act))
+        L.check(L.lib.lssm_inproj_ssd_decode(
+            ctx.h, h_u.data_ptr(), nw.data_ptr(), wi.data_ptr(), si.data_ptr(), cs_u.data_ptr(), cw.data_ptr(),
+            cb.data_ptr(), dtb.data_ptr(), alog.data_ptr(), Dh.data_ptr(), st_u.data_ptr(), yg.data_ptr(),
+            xu.data_ptr(), tag, d_model, d_inner, N, G, H, P, K, 1e-5, wfmt, act))
+        L.check(L.lib.lssm_norm_linear_decode(ctx.h, yg.data_ptr(), mnw.data_ptr(), 1e-5, wo.data_ptr(),
+                                              so.data_ptr(), h_u.data_ptr(), h_u.data_ptr(), 1, d_model,
+                                              d_inner, wfmt, act, O.EPI_ADD))
+        torch.cuda.synchronize()
+        assert torch.equal(cs_f, cs_u), f"conv state, tag {tag}"
+        assert torch.equal(st_f, st_u), f"ssd state, tag {tag}"
+        assert torch.equal(h_f, h_u), f"hidden, tag {tag}: max |d| " \
+            f"{(O.from_act(act_host(h_f, act), act) - O.from_act(act_host(h_u, act), act)).max()}"
+
+
 def test_inproj_ssd_decode_rejects_unsupported(ctx):
     """Shapes the fused launch does not take are refused with nothing run."""
     import lite_ssm_amd as L
