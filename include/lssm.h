@@ -45,7 +45,7 @@ enum {
     LSSM_EINVAL    = 1,  /* bad argument / dimension precondition            */
     LSSM_EDEVICE   = 2,  /* HIP runtime or kernel failure                    */
     LSSM_ESTATE    = 3,  /* batch misuse (begin twice, commit without begin) */
-    LSSM_ENOTFOUND = 4   /* unknown kernel name                              */
+    LSSM_ENOTFOUND = 4   /* unknown kernel name or tensor name              */
 };
 
 /* Activation dtypes.  Codes match the .ssm dtype codes
@@ -391,6 +391,116 @@ int lssm_engine_state(lssm_engine* e, void** conv_state, void** ssd_state);
  * turns both off.  Either pointer may be null.  No counterpart in the
  * reference, whose decode runs every op as its own kernel. */
 int lssm_engine_fused_layers(lssm_engine* e, uint32_t* ssd_fused, uint32_t* mixer_fused);
+
+/* ------------------------------------------------------------------------- */
+/* .ssm weight files                                                          */
+/* ------------------------------------------------------------------------- */
+/* The on-disk format of include/lite_ssm/ssm_format.hpp: a 96-byte header,
+ * n_tensors index entries (32-byte prefix, u64 shape[rank], name bytes, padded
+ * to 8), payloads at 64-byte aligned absolute offsets, all little-endian.
+ * Tensor dtype codes 0-6 are the reference's (ssm_format.hpp:29-41); 7 and 8
+ * are this build's block formats, laid out like DTYPE_INT4_B32 (packed values
+ * of the whole tensor, then its fp16 scales):
+ *   LSSM_DTYPE_Q4_G64: [numel/2 nibble bytes][numel/64 fp16 scales]
+ *   LSSM_DTYPE_Q8_G32: [numel int8 bytes]    [numel/32 fp16 scales]        */
+enum {
+    LSSM_DTYPE_F16 = 0, LSSM_DTYPE_BF16 = 1, LSSM_DTYPE_F32 = 2, LSSM_DTYPE_I8 = 3,
+    LSSM_DTYPE_U8 = 4, LSSM_DTYPE_I32 = 5, LSSM_DTYPE_INT4_B32 = 6,
+    LSSM_DTYPE_Q4_G64 = 7, LSSM_DTYPE_Q8_G32 = 8
+};
+#define LSSM_SSM_MAX_RANK 4   /* TENSOR_MAX_RANK (tensor.hpp:21) */
+
+/* FileHeader (ssm_format.hpp:73-110) without magic and reserved words, plus
+ * the file size.  The writer reads only the hyperparameter fields. */
+typedef struct {
+    uint32_t version, header_size, n_tensors;
+    uint64_t index_offset, data_offset, file_size;
+    uint32_t d_model, n_layer, d_state, d_conv, expand, vocab_size;
+    uint32_t n_heads, d_head, chunk_size, default_dtype, n_groups, norm_before_gate;
+} lssm_ssm_header;
+
+/* One index entry (lite_ssm::Tensor, tensor.hpp:23-36). */
+typedef struct {
+    uint32_t dtype, rank;
+    uint64_t shape[LSSM_SSM_MAX_RANK];  /* unused dims are 0 */
+    uint64_t offset;                    /* absolute byte offset in the file */
+    uint64_t nbytes;
+    const void* host;                   /* payload inside the read-only mapping */
+} lssm_ssm_tensor;
+
+typedef struct lssm_ssm lssm_ssm;
+
+/* Payload bytes of `numel` elements of `dtype`: dtype_packed_nbytes
+ * (ssm_format.hpp:45-69) with codes 7 and 8 added; 0 for an unknown code. */
+uint64_t lssm_ssm_packed_nbytes(uint32_t dtype, uint64_t numel);
+
+/* Map `path` read-only and validate header and index with the checks and
+ * messages of SSMFile::SSMFile (src/core/ssm_loader.cpp:46-138): size, magic,
+ * version, header_size, offsets, rank, in-bounds shape / name / payload, packed
+ * size, duplicate names, index overrunning data_offset.  LSSM_EINVAL on a bad
+ * file, LSSM_EDEVICE (errno text) when it cannot be opened or mapped. */
+int lssm_ssm_open(lssm_ssm** out, const char* path);
+/* Unmaps the file and frees its HBM copy (lssm_ssm_upload). */
+int lssm_ssm_close(lssm_ssm* f);
+/* Header fields; n_groups 0 reads as 1 (ssm_loader.cpp:40). */
+int lssm_ssm_get_header(const lssm_ssm* f, lssm_ssm_header* h);
+/* Entry i in file order; its name (no NUL in the file) is copied into `name`
+ * with a terminating NUL and must fit in `name_cap` bytes. */
+int lssm_ssm_tensor_at(const lssm_ssm* f, uint32_t i, char* name, size_t name_cap,
+                       lssm_ssm_tensor* t);
+/* SSMFile::find / at (ssm_loader.cpp:141-157): LSSM_ENOTFOUND with the
+ * message "SSMFile: no tensor named '<name>'" when absent. */
+int lssm_ssm_find(const lssm_ssm* f, const char* name, lssm_ssm_tensor* t);
+/* Copy the whole file into one HBM allocation, once (the UnifiedBuffer of
+ * metal_buffer.mm:37-67, which wraps the mapping): a tensor's device address
+ * is *device_base + its offset, the reference's (handle, byte offset) pair.
+ * Later calls return the same copy.  Staged through pinned host buffers on the
+ * context's stream; returns when the copy is complete. */
+int lssm_ssm_upload(lssm_ssm* f, lssm_ctx* ctx, void** device_base);
+/* Mamba2Model's weight lookups (mamba2_model.cpp:62-116) against a copy of
+ * the file at `device_base` (the pointer lssm_ssm_upload returned): fills
+ * `cfg` (act from the dtype of backbone.norm_f.weight, wfmt from the dtype of
+ * in_proj), the addresses device_base + offset of embeddings, norm_f and
+ * lm_head (lm_head.weight when present, else the embeddings) and `layers`
+ * (cfg->n_layer entries, at most n_layers_cap; block-format scales follow the
+ * packed values), ready for lssm_engine_create.  Every tensor's dtype, shape
+ * and size is checked against what the engine reads; the reference's messages
+ * for a missing tensor and for in_proj / conv1d dimension mismatches are kept. */
+int lssm_ssm_model(const lssm_ssm* f, const void* device_base, lssm_model_config* cfg,
+                   const void** embed, const void** norm_f, const void** lm_head,
+                   lssm_layer_weights* layers, uint32_t n_layers_cap);
+
+/* Streaming writer (the write path of tools/ssm_format.py): declare every
+ * tensor, then put payloads in any order; the index is written at the first
+ * put (or at finish) and no declaration is accepted after that.  Tensors
+ * never put read as zeros.  After a failed call the writer keeps its first
+ * error; finish returns it, deletes the partial file and frees the writer. */
+typedef struct lssm_ssm_writer lssm_ssm_writer;
+int lssm_ssm_writer_create(lssm_ssm_writer** out, const char* path, const lssm_ssm_header* hp);
+int lssm_ssm_writer_declare(lssm_ssm_writer* w, const char* name, uint32_t dtype, uint32_t rank,
+                            const uint64_t* shape);
+int lssm_ssm_writer_put(lssm_ssm_writer* w, const char* name, const void* data, uint64_t nbytes);
+int lssm_ssm_writer_finish(lssm_ssm_writer* w);
+
+/* Quantize a row-major fp32 [N, K] weight to `wfmt` (Q4_B32, Q4_G64 or Q8_G32)
+ * with the exporter's recipe (tools/export_mamba2.py:68-103): per group,
+ * scale = max(|w|, 1e-12) / qmax in fp32, q = round-half-even(w / scale)
+ * clamped to [qmin, qmax], scale stored fp16; int4 low nibble = even k.
+ * `packed` gets N*K/2 (int4) or N*K (int8) bytes, `scales` N*K/G fp16 bits. */
+int lssm_quantize(const float* w, uint32_t N, uint32_t K, uint32_t wfmt, uint8_t* packed,
+                  uint16_t* scales);
+
+/* Write a random-initialised Mamba-2 model of shape `cfg` (cfg->act: dtype of
+ * embeddings, norms, conv and the per-head parameters; cfg->wfmt: format of
+ * in_proj / out_proj) to `path`, with the reference exporter's tensor names and
+ * order and a tied lm_head (no lm_head.weight).  Values: linears N(0, 0.02)
+ * rounded to fp16 then quantized; embeddings N(0, 0.02); norms N(1, 0.1);
+ * conv weight N(0, 0.3), bias N(0, 0.1); dt_bias = softplus^-1(dt) with dt
+ * log-uniform in [1e-3, 1e-1]; A_log = log(1 + 15u); D N(1, 0.1).  Normals
+ * come from std::mt19937_64 streams keyed by (seed, tensor, block) through the
+ * Box-Muller transform in fp64, so the file depends only on cfg and seed.
+ * No counterpart in the reference, which exports trained checkpoints. */
+int lssm_ssm_write_random(const char* path, const lssm_model_config* cfg, uint64_t seed);
 
 #ifdef __cplusplus
 }

@@ -18,7 +18,8 @@ __all__ = [
     "LIB_PATH", "lib", "LssmError", "Ctx", "check", "F16", "BF16", "F32",
     "W_DENSE", "W_Q4_B32", "W_Q4_G64", "W_Q8_G32", "EPI_NONE", "EPI_SILU", "EPI_ADD",
     "LinearDims", "RMSNormDims", "RMSLinearDims", "Conv1dDims", "SSDDims", "SSDStepDims",
-    "FusedInProjDims", "ModelConfig", "LayerWeights", "exported_symbols",
+    "FusedInProjDims", "ModelConfig", "LayerWeights", "SsmHeader", "SsmTensor",
+    "exported_symbols",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -81,6 +82,21 @@ class LayerWeights(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in
                 ("norm_w", "in_proj_w", "in_proj_s", "conv1d_w", "conv1d_b", "dt_bias", "A_log",
                  "D", "mixer_norm_w", "out_proj_w", "out_proj_s")]
+
+
+class SsmHeader(C.Structure):
+    """lssm_ssm_header: .ssm FileHeader fields (include/lite_ssm/ssm_format.hpp:73-110)."""
+    _fields_ = ([(n, C.c_uint32) for n in ("version", "header_size", "n_tensors")] +
+                [(n, C.c_uint64) for n in ("index_offset", "data_offset", "file_size")] +
+                [(n, C.c_uint32) for n in
+                 ("d_model", "n_layer", "d_state", "d_conv", "expand", "vocab_size", "n_heads",
+                  "d_head", "chunk_size", "default_dtype", "n_groups", "norm_before_gate")])
+
+
+class SsmTensor(C.Structure):
+    """lssm_ssm_tensor: one index entry (lite_ssm::Tensor)."""
+    _fields_ = [("dtype", C.c_uint32), ("rank", C.c_uint32), ("shape", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("host", C.c_void_p)]
 
 
 _vp, _u32, _i, _f, _sz = C.c_void_p, C.c_uint32, C.c_int, C.c_float, C.c_size_t
@@ -156,6 +172,22 @@ _SIGS = {
     "lssm_engine_logits": ([_vp, C.POINTER(_vp)], _i),
     "lssm_engine_state": ([_vp, C.POINTER(_vp), C.POINTER(_vp)], _i),
     "lssm_engine_fused_layers": ([_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)], _i),
+    # .ssm files
+    "lssm_ssm_packed_nbytes": ([_u32, C.c_uint64], C.c_uint64),
+    "lssm_ssm_open": ([C.POINTER(_vp), C.c_char_p], _i),
+    "lssm_ssm_close": ([_vp], _i),
+    "lssm_ssm_get_header": ([_vp, C.POINTER(SsmHeader)], _i),
+    "lssm_ssm_tensor_at": ([_vp, _u32, C.c_char_p, _sz, C.POINTER(SsmTensor)], _i),
+    "lssm_ssm_find": ([_vp, C.c_char_p, C.POINTER(SsmTensor)], _i),
+    "lssm_ssm_upload": ([_vp, _vp, C.POINTER(_vp)], _i),
+    "lssm_ssm_model": ([_vp, _vp, C.POINTER(ModelConfig), C.POINTER(_vp), C.POINTER(_vp),
+                        C.POINTER(_vp), C.POINTER(LayerWeights), _u32], _i),
+    "lssm_ssm_writer_create": ([C.POINTER(_vp), C.c_char_p, C.POINTER(SsmHeader)], _i),
+    "lssm_ssm_writer_declare": ([_vp, C.c_char_p, _u32, _u32, C.POINTER(C.c_uint64)], _i),
+    "lssm_ssm_writer_put": ([_vp, C.c_char_p, _vp, C.c_uint64], _i),
+    "lssm_ssm_writer_finish": ([_vp], _i),
+    "lssm_quantize": ([_vp, _u32, _u32, _u32, _vp, _vp], _i),
+    "lssm_ssm_write_random": ([C.c_char_p, C.POINTER(ModelConfig), C.c_uint64], _i),
 }
 
 

@@ -200,13 +200,16 @@ class DeviceModel:
 class Engine:
     """lssm_engine wrapper: prefill / decode / graph-replayed decode."""
 
-    def __init__(self, ctx, model: DeviceModel, max_batch: int, max_seq: int):
+    def __init__(self, ctx, model, max_batch: int, max_seq: int):
+        """`model`: a DeviceModel, or the FileModel of an uploaded .ssm file
+        (lite_ssm_amd.ssm), whose tensors are device addresses (ints)."""
         self.ctx, self.model = ctx, model
         self._cfg = model.config()
         self._layers = model.layer_structs()
+        ptr = lambda t: t if isinstance(t, int) else t.data_ptr()  # noqa: E731
         h = C.c_void_p()
-        check(lib.lssm_engine_create(C.byref(h), ctx.h, C.byref(self._cfg), model.embed.data_ptr(),
-                                     model.norm_f.data_ptr(), model.lm_head.data_ptr(),
+        check(lib.lssm_engine_create(C.byref(h), ctx.h, C.byref(self._cfg), ptr(model.embed),
+                                     ptr(model.norm_f), ptr(model.lm_head),
                                      self._layers, max_batch, max_seq))
         self.h = h
         self.max_batch, self.max_seq = max_batch, max_seq
