@@ -163,6 +163,12 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
     const uint32_t RS = K / 2 + 4;                             // x row pitch (dwords)
     const uint32_t KO = K / 8;                                 // octets per row
     const uint32_t SEG = (KO + 63) / 64;                       // 64-octet segments per row
+    // segment u -> (row u / SEG, place u % SEG) by one multiply-high: exact
+    // for u, SEG < 2^16 with ceil(2^32 / SEG) (a division per segment costs
+    // ~15 scalar instructions, and the staging is issue-bound)
+    const uint32_t seg_magic = SEG == 1 ? 0u : 0xFFFFFFFFu / SEG + 1u;
+    auto seg_row = [&](uint32_t u) -> uint32_t { return SEG == 1 ? u : __umulhi(u, seg_magic); };
+    auto seg_at = [&](uint32_t u) -> uint32_t { return u - seg_row(u) * SEG; };
     uint32_t* xl = mm_lds;
     const uint32_t tiles = (N + 15) / 16;
     const uint32_t tile0 = blockIdx.x * CT;
@@ -192,7 +198,7 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
         asm volatile("" : "+v"(lane));
         auto load = [&](int j, u32x4& xv, u32x4& nv) {
             const uint32_t u = w + KS * j;
-            const uint32_t m = min(base + u / SEG, M - 1), cc = min((u % SEG) * 64 + lane, KO - 1);
+            const uint32_t m = min(base + seg_row(u), M - 1), cc = min(seg_at(u) * 64 + lane, KO - 1);
             xv = *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(c.x) + (size_t)m * c.x_stride + 8 * cc);
             if constexpr (NORM) nv = reinterpret_cast<const u32x4*>(c.norm_w)[cc];
         };
@@ -206,7 +212,7 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
                 q = dot2(d[1], d[1], q, T{});
                 q = dot2(d[2], d[2], q, T{});
                 q = dot2(d[3], d[3], q, T{});
-                part[u * WAVE + lane] = (u % SEG) * 64 + lane < KO ? q : 0.0f;
+                part[u * WAVE + lane] = seg_at(u) * 64 + lane < KO ? q : 0.0f;
             };
             if constexpr (KEEP) {
 #pragma unroll
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
         }
         auto put = [&](int j, const u32x4& xv, const u32x4& nv, float rr) {
             const uint32_t u = w + KS * j;
-            const uint32_t r = u / SEG, cc = (u % SEG) * 64 + lane;
+            const uint32_t r = seg_row(u), cc = seg_at(u) * 64 + lane;
             const bool live = cc < KO;
             float v[8];
             if constexpr (NORM) {
@@ -268,7 +274,7 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
             for (int j = 0; j < MM_MAXJ; ++j) {
                 rr[j] = 1.0f;
                 if constexpr (NORM) {
-                    if (w + KS * j < nseg) rr[j] = rinv_s[(w + KS * j) / SEG];
+                    if (w + KS * j < nseg) rr[j] = rinv_s[seg_row(w + KS * j)];
                 }
             }
 #pragma unroll
@@ -284,7 +290,7 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
                     rr[jj] = 1.0f;
                     if (w + KS * (j0 + jj) < nseg) {
                         load(j0 + jj, xv[jj], nv[jj]);
-                        if constexpr (NORM) rr[jj] = rinv_s[(w + KS * (j0 + jj)) / SEG];
+                        if constexpr (NORM) rr[jj] = rinv_s[seg_row(w + KS * (j0 + jj))];
                     }
                 }
 #pragma unroll
@@ -350,7 +356,7 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
         for (int j = 0; j < MM_MAXJ; ++j) {
             const uint32_t u = w + KS * j;
             if (u < nseg) {
-                const uint32_t m = min(u / SEG, M - 1), cc = min((u % SEG) * 64 + lane0, KO - 1);
+                const uint32_t m = min(seg_row(u), M - 1), cc = min(seg_at(u) * 64 + lane0, KO - 1);
                 xk[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(c.x) + (size_t)m * c.x_stride + 8 * cc);
                 if constexpr (NORM) {
                     if (j == 0 || !one_place) nk[j] = reinterpret_cast<const u32x4*>(c.norm_w)[cc];
