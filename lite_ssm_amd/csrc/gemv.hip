@@ -359,8 +359,8 @@ template <typename T, int FMT, int LPR2, int CPL2> struct EpiLayer {
                 float v[8];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    v[2 * q] = dot2(xd[q], wd[q] & 0x0000FFFFu, 0.0f, T{}) * rr;
-                    v[2 * q + 1] = dot2(xd[q], wd[q] & 0xFFFF0000u, 0.0f, T{}) * rr;
+                    v[2 * q] = lo_f<T>(xd[q]) * lo_f<T>(wd[q]) * rr;
+                    v[2 * q + 1] = hi_f<T>(xd[q]) * hi_f<T>(wd[q]) * rr;
                 }
                 // the octet's offset in its chunk as a constant (a runtime
                 // index into v would put it in scratch)
@@ -599,14 +599,14 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
                 const T* t = reinterpret_cast<const T*>(&xo[m][i]);
                 float v[8];
                 if constexpr (NORM) {
-                    // x * w exactly (v_dot2 of a pair with one half of the other
-                    // pair masked), then * 1/rms: the fp32 products of the reference
+                    // x * w exactly (a product of 8- or 11-bit significands in
+                    // fp32), then * 1/rms: the fp32 products of the reference
                     const uint32_t* xd = reinterpret_cast<const uint32_t*>(&xo[m][i]);
                     const uint32_t* wd = reinterpret_cast<const uint32_t*>(&wo[i]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        v[2 * e] = dot2(xd[e], wd[e] & 0x0000FFFFu, 0.0f, T{}) * rr[m];
-                        v[2 * e + 1] = dot2(xd[e], wd[e] & 0xFFFF0000u, 0.0f, T{}) * rr[m];
+                        v[2 * e] = lo_f<T>(xd[e]) * lo_f<T>(wd[e]) * rr[m];
+                        v[2 * e + 1] = hi_f<T>(xd[e]) * hi_f<T>(wd[e]) * rr[m];
                     }
                 } else {
 #pragma unroll

@@ -259,6 +259,18 @@ template <typename T> __device__ __forceinline__ uint32_t bits16(T v) {
 template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return bits16(from_f<T>(a)) | (bits16(from_f<T>(b)) << 16);
 }
+// bf16: one v_cvt_pk_bf16_f32 for the pair (round to nearest even, as the
+// conversion of each value alone)
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2p __attribute__((ext_vector_type(2)));
+template <> __device__ __forceinline__ uint32_t pack2<bf16>(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, bf16x2p));
+}
+// fp32 value of the low / high 16-bit half of a packed pair
+template <typename T> __device__ __forceinline__ float lo_f(uint32_t u) { return f_of_bits<T>((uint16_t)(u & 0xFFFFu)); }
+template <typename T> __device__ __forceinline__ float hi_f(uint32_t u) { return f_of_bits<T>((uint16_t)(u >> 16)); }
+template <> __device__ __forceinline__ float lo_f<bf16>(uint32_t u) { return __uint_as_float(u << 16); }
+template <> __device__ __forceinline__ float hi_f<bf16>(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c, f16) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, a), __builtin_bit_cast(half2v, b), c, false);
 }

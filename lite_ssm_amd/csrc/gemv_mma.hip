@@ -245,10 +245,11 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
             const bool live = cc < KO;
             float v[8];
             if constexpr (NORM) {
+                // x w is exact in fp32 (products of 8- or 11-bit significands), then * rr
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    v[2 * e] = dot2(xv[e], nv[e] & 0x0000FFFFu, 0.0f, T{}) * rr;
-                    v[2 * e + 1] = dot2(xv[e], nv[e] & 0xFFFF0000u, 0.0f, T{}) * rr;
+                    v[2 * e] = lo_f<T>(xv[e]) * lo_f<T>(nv[e]) * rr;
+                    v[2 * e + 1] = hi_f<T>(xv[e]) * hi_f<T>(nv[e]) * rr;
                 }
             } else {
 #pragma unroll
