@@ -55,7 +55,7 @@ struct lssm_engine {
     void* d_xbc = nullptr;
     void* d_dt = nullptr;
     void* d_g = nullptr;
-    void* d_gn = nullptr;
+    void* d_gn = nullptr;      // also the packed x rows of the MFMA decode GEMV (launch_mma_pack)
     void* logits = nullptr;
     void* conv_state = nullptr;
     float* ssd_state = nullptr;
@@ -68,6 +68,9 @@ struct lssm_engine {
     uint64_t* xfer = nullptr;
     uint32_t* seq = nullptr;
     bool fuse_ssd = true;
+    // decode batches from this many rows pack x once per linear (launch_mma_pack);
+    // LSSM_PACK_MIN_ROWS at creation overrides it
+    uint32_t pack_min_rows = 8;
     // LSSM_FUSED_MIXER=1: out_proj in the same launch too (bit-identical; on
     // the 2.7B shape it measures ~3 % slower than a separate out_proj launch:
     // its two waits on other workgroups' words cost more than one kernel
@@ -148,6 +151,13 @@ struct lssm_engine {
                               (B >= 2 && gemv_mma_takes(B, proj, d_model, wfmt, act));
         const bool fused_out = (B <= 4 && gemv_max_rows(d_inner, wfmt, act) >= 1) ||
                                (B >= 2 && gemv_mma_takes(B, d_model, d_inner, wfmt, act));
+        // 8 rows or more: x is normalised and packed once per linear (into
+        // d_gn) instead of by every block of the MFMA GEMV, whose staging is
+        // issue-bound (below 8 rows the extra launch costs what it saves)
+        const uint32_t PACK_MIN_ROWS = pack_min_rows;
+        const bool pack_in = B >= PACK_MIN_ROWS && d_model % 128 == 0 && gemv_mma_takes(B, proj, d_model, wfmt, act);
+        const bool pack_out = B >= PACK_MIN_ROWS && d_inner % 128 == 0 &&
+                              gemv_mma_takes(B, d_model, d_inner, wfmt, act);
         fused_layers = 0;
         mixer_layers = 0;
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
@@ -182,7 +192,11 @@ struct lssm_engine {
                     fused_layers += ssd_done ? 1u : 0u;
                     mixer_layers += out_done ? 1u : 0u;
                 }
-                if (!ssd_done) e = launch_inproj_decode(st(), a);
+                if (!ssd_done && pack_in) {
+                    e = launch_mma_pack(st(), d_hidden, d_model, w.norm_w, RMS_EPS, B, d_model, wfmt, act, d_gn);
+                    a.g.xpack = d_gn;
+                }
+                if (!ssd_done && e == hipSuccess) e = launch_inproj_decode(st(), a);
             } else {
                 e = launch_rmsnorm(st(), d_hidden, d_model, w.norm_w, d_normed, d_model, B, d_model,
                                    RMS_EPS, act);
@@ -209,7 +223,11 @@ struct lssm_engine {
             if (fused_out) {
                 GemvArgs g{d_g, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden,
                            w.mixer_norm_w, RMS_EPS, B, d_model, d_inner, wfmt, act, LSSM_EPI_ADD};
-                e = launch_gemv(st(), g);
+                if (pack_out) {
+                    e = launch_mma_pack(st(), d_g, d_inner, w.mixer_norm_w, RMS_EPS, B, d_inner, wfmt, act, d_gn);
+                    g.xpack = d_gn;
+                }
+                if (e == hipSuccess) e = launch_gemv(st(), g);
             } else {
                 e = launch_rmsnorm(st(), d_g, d_inner, w.mixer_norm_w, d_gn, d_inner, B, d_inner,
                                    RMS_EPS, act);
@@ -404,6 +422,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     }
     if (const char* v = getenv("LSSM_FUSED_SSD")) e->fuse_ssd = v[0] != '0';
     if (const char* v = getenv("LSSM_FUSED_MIXER")) e->fuse_mixer = v[0] == '1';
+    if (const char* v = getenv("LSSM_PACK_MIN_ROWS")) e->pack_min_rows = (uint32_t)strtoul(v, nullptr, 10);
     if (rc != LSSM_OK) {
         delete e;
         return rc;

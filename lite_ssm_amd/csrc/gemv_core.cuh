@@ -28,6 +28,9 @@ struct GemvCore {
     float eps;
     uint32_t N, K;
     float inv_k;                                     // 1 / K (the RMSNorm mean)
+    // the MFMA decode GEMV only: x already normalised and packed in its
+    // staging order ([M][K / 2] dwords, launch_mma_pack), or null
+    const uint32_t* xp = nullptr;
 };
 
 template <int FMT, typename T> struct Fmt;

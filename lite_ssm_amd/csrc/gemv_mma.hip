@@ -146,7 +146,7 @@ template <typename T> __device__ __forceinline__ floatx4 mfma16(u32x4 a, u32x4 b
 
 // ra: dwords of the LDS region that holds, in turn, the lanes' sums of
 // squares, the staged x rows and each pass's partial sums.
-template <int FMT, typename T, int CT, int QPW, bool NORM, class Epi>
+template <int FMT, typename T, int CT, int QPW, bool NORM, bool PACKED, class Epi>
 __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvCore c, Epi epi, uint32_t M, uint32_t mpb,
                                                                  uint32_t ra) {
     using P = Mma<FMT, T>;
@@ -303,6 +303,34 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
         lds_barrier();
     };
 
+    // ---- x pre-packed by launch_mma_pack: rows [base, base + mpb) copied ----
+    // (16-byte pieces p = row * KO + octet, eight in flight per thread)
+    auto copy_in = [&](uint32_t base) {
+        const uint32_t NT = blockDim.x, KH = K / 2;
+        const uint32_t n = min(mpb, M - base) * KO;
+        const uint32_t ko_magic = 0xFFFFFFFFu / KO + 1u;           // KO >= 16: exact for p < 2^16
+        for (uint32_t p0 = threadIdx.x; p0 < n; p0 += 8 * NT) {
+            u32x4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t p = p0 + i * NT;
+                if (p < n) {
+                    const uint32_t r = __umulhi(p, ko_magic), cc = p - r * KO;
+                    v[i] = *reinterpret_cast<const u32x4*>(c.xp + (size_t)(base + r) * KH + 4 * cc);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t p = p0 + i * NT;
+                if (p < n) {
+                    const uint32_t r = __umulhi(p, ko_magic), cc = p - r * KO;
+                    *reinterpret_cast<u32x4*>(xl + r * RS + 4 * cc) = v[i];
+                }
+            }
+        }
+        lds_barrier();
+    };
+
     // ---- weights (and raw scale bits) of the wave's quads, all in flight ----
     // With few weight registers (CT * QPW <= 8) they are held over all
     // passes; otherwise a later pass reads them again (L2 hits) rather than
@@ -346,7 +374,8 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
     // x of the first pass, staged before any weight is requested: requested
     // behind the weights, x would queue behind the whole chip's weight
     // traffic (measured: staging done ~7 us after the start instead of ~2)
-    const bool keep0 = mpb * SEG <= (uint32_t)(MM_MAXJ * KS);   // the first pass's x fits the registers
+    constexpr bool packed = PACKED;                            // x from launch_mma_pack (c.xp)
+    const bool keep0 = !packed && mpb * SEG <= (uint32_t)(MM_MAXJ * KS);   // the first pass's x fits the registers
     if (keep0) {
         const uint32_t nseg = mpb * SEG;
         const uint32_t lane0 = threadIdx.x % WAVE;
@@ -366,13 +395,15 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
             }
         }
     }
-    if (keep0) stage(0u, FmtTag<1>{});
+    if (packed) copy_in(0u);
+    else if (keep0) stage(0u, FmtTag<1>{});
     else stage(0u, FmtTag<0>{});
     load_w();
 
     for (uint32_t base = 0; base < M; base += mpb) {
         if (base > 0) {
-            stage(base, FmtTag<0>{});
+            if (packed) copy_in(base);
+            else stage(base, FmtTag<0>{});
             if constexpr (!HOLD) load_w();
         }
         const uint32_t rows = min(mpb, M - base);
@@ -529,9 +560,9 @@ template <typename T> bool mma_aligned(const GemvCore& c, bool norm) {
            (!norm || (uintptr_t)c.norm_w % 16 == 0) && (uintptr_t)c.w % 16 == 0 && (uintptr_t)c.s % 16 == 0;
 }
 
-template <int FMT, typename T, int CT, int QPW, bool NORM, class Epi>
+template <int FMT, typename T, int CT, int QPW, bool NORM, bool PACKED, class Epi>
 hipError_t mma_run(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmaPlan& p) {
-    auto k = gemv_mma_kernel<FMT, T, CT, QPW, NORM, Epi>;
+    auto k = gemv_mma_kernel<FMT, T, CT, QPW, NORM, PACKED, Epi>;
     // opt in to the dynamic LDS once per instantiation (a host attribute)
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)MM_LDS_MAX);
@@ -541,22 +572,22 @@ hipError_t mma_run(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, c
     return hipGetLastError();
 }
 
-template <int FMT, typename T, bool NORM, class Epi>
+template <int FMT, typename T, bool NORM, bool PACKED, class Epi>
 hipError_t mma_shape(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmaPlan& p) {
     if (p.ct == 1) {
         switch (p.qpw) {
-            case 1: return mma_run<FMT, T, 1, 1, NORM, Epi>(s, c, e, M, p);
-            case 2: return mma_run<FMT, T, 1, 2, NORM, Epi>(s, c, e, M, p);
-            case 4: return mma_run<FMT, T, 1, 4, NORM, Epi>(s, c, e, M, p);
-            default: return mma_run<FMT, T, 1, 8, NORM, Epi>(s, c, e, M, p);
+            case 1: return mma_run<FMT, T, 1, 1, NORM, PACKED, Epi>(s, c, e, M, p);
+            case 2: return mma_run<FMT, T, 1, 2, NORM, PACKED, Epi>(s, c, e, M, p);
+            case 4: return mma_run<FMT, T, 1, 4, NORM, PACKED, Epi>(s, c, e, M, p);
+            default: return mma_run<FMT, T, 1, 8, NORM, PACKED, Epi>(s, c, e, M, p);
         }
     }
     if constexpr (FMT == LSSM_W_Q4_G64 || FMT == LSSM_W_Q4_B32) {
-        if (p.qpw == 4) return mma_run<FMT, T, 4, 4, NORM, Epi>(s, c, e, M, p);
+        if (p.qpw == 4) return mma_run<FMT, T, 4, 4, NORM, PACKED, Epi>(s, c, e, M, p);
         switch (p.ct) {
-            case 2: return mma_run<FMT, T, 2, 2, NORM, Epi>(s, c, e, M, p);
-            case 3: return mma_run<FMT, T, 3, 2, NORM, Epi>(s, c, e, M, p);
-            default: return mma_run<FMT, T, 4, 2, NORM, Epi>(s, c, e, M, p);
+            case 2: return mma_run<FMT, T, 2, 2, NORM, PACKED, Epi>(s, c, e, M, p);
+            case 3: return mma_run<FMT, T, 3, 2, NORM, PACKED, Epi>(s, c, e, M, p);
+            default: return mma_run<FMT, T, 4, 2, NORM, PACKED, Epi>(s, c, e, M, p);
         }
     }
     return hipErrorInvalidValue;                       // not a planned shape
@@ -592,7 +623,8 @@ bool try_mma(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, int wfm
         constexpr int FMT = decltype(tag)::value;
         MmaPlan p;
         if (!mma_plan<FMT, T>(M, c.N, c.K, p)) return false;
-        err = mma_shape<FMT, T, true, Epi>(s, c, e, M, p);
+        err = c.xp ? mma_shape<FMT, T, true, true, Epi>(s, c, e, M, p)
+                   : mma_shape<FMT, T, true, false, Epi>(s, c, e, M, p);
         return true;
     });
 }
@@ -604,7 +636,75 @@ template <typename T> bool mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfm
     });
 }
 
+// ---- x normalised and packed once for a whole gemv_mma launch ----
+// Row m: rr = 1 / sqrt(mean(x^2) + eps), then each octet's r(x w rr) in the
+// staging's pair order (norm.metal:52-79), stored as the staging would put it
+// in LDS (pairs of k .. k + 7 at dwords k / 2 .. k / 2 + 3 of the row).
+template <int FMT, typename T>
+__global__ __launch_bounds__(1024) void mma_pack_kernel(const T* x, uint32_t x_stride, const T* nw, float eps,
+                                                        uint32_t K, uint32_t* out) {
+    // one octet per thread (blockDim.x >= K / 8), x and w read once
+    __shared__ float red[1024 / WAVE];
+    const uint32_t m = blockIdx.x, KO = K / 8, cc = threadIdx.x;
+    const bool live = cc < KO;
+    u32x4 xv = u32x4{0u, 0u, 0u, 0u}, nv = xv;
+    if (live) {
+        xv = reinterpret_cast<const u32x4*>(x + (size_t)m * x_stride)[cc];
+        nv = reinterpret_cast<const u32x4*>(nw)[cc];
+    }
+    float q = dot2(xv[0], xv[0], 0.0f, T{});
+    q = dot2(xv[1], xv[1], q, T{});
+    q = dot2(xv[2], xv[2], q, T{});
+    q = dot2(xv[3], xv[3], q, T{});
+    // block sum in a fixed order: waves, then the wave sums in wave order
+    q = wave_sum(q);
+    const uint32_t nwv = blockDim.x / WAVE;
+    if (threadIdx.x % WAVE == 0) red[threadIdx.x / WAVE] = q;
+    __syncthreads();
+    float t = 0.0f;
+    for (uint32_t i = 0; i < nwv; ++i) t += red[i];
+    const float rr = 1.0f / sqrtf(t / (float)K + eps);
+    if (!live) return;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        v[2 * e] = lo_f<T>(xv[e]) * lo_f<T>(nv[e]) * rr;
+        v[2 * e + 1] = hi_f<T>(xv[e]) * hi_f<T>(nv[e]) * rr;
+    }
+    u32x4 pk;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+        int pa, pb;
+        octet_pos<FMT, T>(qq, pa, pb);
+        pk[qq] = pack2<T>(v[pa], v[pb]);
+    }
+    reinterpret_cast<u32x4*>(out + (size_t)m * (K / 2))[cc] = pk;
+}
+
 }  // namespace
+
+hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, const void* norm_w, float eps,
+                           uint32_t M, uint32_t K, int wfmt, int act, void* out) {
+    if (M == 0 || K % 128 != 0 || K > 8192 || (uintptr_t)x % 16 || (x_stride * 2u) % 16 ||
+        (uintptr_t)norm_w % 16 || (uintptr_t)out % 16)
+        return hipErrorInvalidValue;
+    const uint32_t nt = (K / 8 + WAVE - 1) / WAVE * WAVE;      // one octet per thread
+    hipError_t err = hipErrorInvalidValue;
+    auto go = [&](auto tag) -> bool {
+        using T = decltype(tag);
+        return mma_fmt<T>(wfmt, [&](auto ft) -> bool {
+            constexpr int FMT = decltype(ft)::value;
+            mma_pack_kernel<FMT, T><<<M, nt, 0, s>>>(static_cast<const T*>(x), x_stride,
+                                                      static_cast<const T*>(norm_w), eps, K,
+                                                      static_cast<uint32_t*>(out));
+            err = hipGetLastError();
+            return true;
+        });
+    };
+    if (act == LSSM_F16) go(f16{});
+    else if (act == LSSM_BF16) go(bf16{});
+    return err;
+}
 
 bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
     if (act == LSSM_F16) return mma_takes<f16>(M, N, K, wfmt);
@@ -615,6 +715,7 @@ bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
 bool launch_gemv_mma(hipStream_t s, const GemvArgs& a, hipError_t& err) {
     if (a.M < 2) return false;
     GemvCore c{a.x, a.x_stride, (const uint8_t*)a.w, (const uint16_t*)a.s, a.norm_w, a.eps, a.N, a.K, 1.0f / (float)a.K};
+    c.xp = static_cast<const uint32_t*>(a.xpack);
     auto go = [&](auto tag) -> bool {
         using T = decltype(tag);
         EpiPlain<T> e{(T*)a.y, a.y_stride, (const T*)a.res, a.epi};
@@ -629,6 +730,7 @@ bool launch_inproj_decode_mma(hipStream_t s, const InprojDecodeArgs& a, hipError
     const GemvArgs& g = a.g;
     if (g.M < 2) return false;
     GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
+    c.xp = static_cast<const uint32_t*>(g.xpack);
     auto go = [&](auto tag) -> bool {
         using T = decltype(tag);
         EpiInproj<T> e{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,

@@ -106,6 +106,9 @@ struct GemvArgs {
     float eps;
     uint32_t M, N, K;
     int wfmt, act, epi;
+    // x rows as launch_mma_pack wrote them (norm_w applied), or null; used by
+    // the MFMA decode GEMV, which then copies instead of normalising
+    const void* xpack = nullptr;
 };
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a);
 // Rows of x one GEMV launch can take for this K / format (0 = none), with
@@ -218,5 +221,10 @@ bool launch_inproj_decode_mma(hipStream_t s, const InprojDecodeArgs& a, hipError
 // Whether a decode batch of M rows runs in one MFMA launch (16-byte aligned
 // operands assumed; otherwise the launchers fall back to gemv1 launches).
 bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);
+// RMSNorm of M rows of x (K, 16-bit act), rounded and packed in the MFMA
+// decode GEMV's staging order for `wfmt`, into out ([M][K / 2] dwords): one
+// pass for all blocks of the GEMV launch that follows (GemvArgs::xpack).
+hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, const void* norm_w,
+                           float eps, uint32_t M, uint32_t K, int wfmt, int act, void* out);
 
 }  // namespace lssm
