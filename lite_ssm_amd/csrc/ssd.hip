@@ -58,7 +58,7 @@ __global__ __launch_bounds__(ST_NT) void ssd_step_kernel(SsdArgs a) {
     f32x4 s[F];
     T4 bv[F], cv[F];
 #pragma unroll
-    for (int f = 0; f < F; ++f) s[f] = S[lr + ST_NV * f];
+    for (int f = 0; f < F; ++f) s[f] = __builtin_nontemporal_load(&S[lr + ST_NV * f]);   // streamed once
 #pragma unroll
     for (int f = 0; f < F; ++f) {
         bv[f] = B4[lr + ST_NV * f];
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(ST_NT) void ssd_step_kernel(SsdArgs a) {
         t.y = fmaf(decay, t.y, dt * to_f(bv[f].y) * xv);
         t.z = fmaf(decay, t.z, dt * to_f(bv[f].z) * xv);
         t.w = fmaf(decay, t.w, dt * to_f(bv[f].w) * xv);
-        S[lr + ST_NV * f] = t;
+        __builtin_nontemporal_store(t, &S[lr + ST_NV * f]);
         ys += fmaf(to_f(cv[f].w), t.w, fmaf(to_f(cv[f].z), t.z, fmaf(to_f(cv[f].x), t.x, to_f(cv[f].y) * t.y)));
     }
     ys = group_sum<ST_NV>(ys);
