@@ -202,16 +202,25 @@ def main():
         print(f"[bench] decode bs={b}: {tbt / n * 1e3:.3f} ms/step", file=sys.stderr, flush=True)
 
     # ---------------- dominant kernel, live (HIP events on the library's stream) ----------------
+    # (shapes the fused launch does not take, e.g. 8B with more workgroups than
+    # CUs, decode through separate launches: roofline is then null)
+    roof = None
     run = fused_launcher(L, ctx, m, sh, fused_buffers(sh))
     ctx.begin_batch()
-    run()
-    reps = 10
-    t_k = timed(run, reps)
-    ctx.commit_and_wait()
-    k_us = t_k / (reps * sh.n_layer) * 1e6
-    k_bytes = fused_bytes(m, sh)
-    achieved = k_bytes / (k_us * 1e-6) / 1e9
-    print(f"[bench] inproj_ssd_decode: {k_us:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+    try:
+        run()
+        reps = 10
+        t_k = timed(run, reps)
+    except L.LssmError as err:
+        t_k = None
+        print(f"[bench] inproj_ssd_decode not measured: {err}", file=sys.stderr, flush=True)
+    finally:
+        ctx.commit_and_wait()
+    if t_k is not None:
+        k_us = t_k / (reps * sh.n_layer) * 1e6
+        k_bytes = fused_bytes(m, sh)
+        achieved = k_bytes / (k_us * 1e-6) / 1e9
+        print(f"[bench] inproj_ssd_decode: {k_us:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
     # ---------------- CPU baseline (oracle, bounded sample) ----------------
     cpu = None
@@ -237,12 +246,21 @@ def main():
                          f"(C, OpenMP {nthr} threads)"}
         print(f"[bench] cpu oracle: {ct / args.cpu_steps:.2f} s/token", file=sys.stderr, flush=True)
 
+    if t_k is not None:
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "inproj_ssd_decode (RMSNorm + in_proj int4-g64 GEMV + conv update + SiLU "
+                          "+ SSD step + SiLU(z) gate, one launch per layer)",
+                "bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_us, 3)}
+
     # HBM bytes per launch of the same kernel from the two rocprofv3 --pmc passes
     # (FETCH_SIZE, WRITE_SIZE, calibrated on a 256 MiB copy), recorded in profiles/
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "inproj_ssd_decode_traffic.json")
     if args.model == "mamba2-2.7b" and os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("traffic_bytes")
+    if roof is not None:
+        roof["traffic"] = traffic
 
     out = {
         "metric": "decode tok/s (bs=1) + prefill tok/s, Mamba-2-2.7B int4; % HBM/MFMA roofline",
@@ -261,11 +279,7 @@ def main():
                                f"batch 1 (BASELINE config 4), random-init weights in HBM",
                    "layers": sh.n_layer, "d_model": sh.d_model, "vocab": sh.vocab_size,
                    "batch": 1, "prefill": f"{PB}x{PL}"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "inproj_ssd_decode (RMSNorm + in_proj int4-g64 GEMV + conv update + SiLU "
-                               "+ SSD step + SiLU(z) gate, one launch per layer)",
-                     "bytes_per_launch": int(k_bytes), "avg_launch_us": round(k_us, 3)},
+        "roofline": roof,
         "cpu_baseline": cpu,
         "step_hbm_frac": round((wbytes + 2 * state_bytes) / (t_dec / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
         "step_bytes": int(wbytes + 2 * state_bytes),
