@@ -113,6 +113,23 @@ int lssm_commit_and_wait(lssm_ctx* ctx);   /* MetalOps::commit_and_wait ops.hpp:
 int lssm_batch_active(lssm_ctx* ctx);      /* MetalOps::batch_active  ops.hpp:93 */
 int lssm_sync(lssm_ctx* ctx);              /* stream sync + error check          */
 
+/* Every synchronisation point of a context (lssm_sync, lssm_commit_and_wait,
+ * and any op outside a batch) also reads a device status word that kernels
+ * set for conditions they cannot report otherwise, and clears it:
+ *   - a token id outside [0, vocab) reached the embedding (ids live in device
+ *     memory, so the check of mamba2_model.cpp:129-131 runs there):
+ *     LSSM_EINVAL, "Mamba2Model::embed: token_id out of range";
+ *   - a bounded cross-workgroup wait of a fused decode launch gave up (its
+ *     workgroups were not all resident at once): LSSM_EDEVICE; the affected
+ *     outputs are NaN and their SSD state is left as it was.
+ *
+ * Failure-injection switches for the tests of these paths (no counterpart in
+ * the reference; 0 = off, the default).  LSSM_DEBUG_STALE_WAIT makes the SSD
+ * items of lssm_inproj_ssd_decode wait for a tag that no workgroup publishes,
+ * so every bounded wait gives up and the kernel still exits normally. */
+#define LSSM_DEBUG_STALE_WAIT 1u
+int lssm_ctx_set_debug(lssm_ctx* ctx, uint32_t flags);
+
 /* MetalOps::metallib_loaded / has_pipeline / metallib_path (ops.hpp:66-74). */
 int lssm_library_loaded(void);
 int lssm_has_kernel(const char* name);
@@ -382,6 +399,15 @@ int lssm_engine_decode_graph(lssm_engine* e, const int32_t* ids, uint32_t batch,
                              int32_t* next_ids, uint32_t steps);
 /* Device pointers to engine buffers (valid until destroy). */
 int lssm_engine_logits(lssm_engine* e, void** logits);          /* [max_batch, vocab] act */
+/* Parity hook, no counterpart in the reference (it is for layer-by-layer
+ * comparisons against a CPU restatement of run_block).  With `buf` set, each
+ * later lssm_engine_prefill / lssm_engine_decode copies the hidden rows
+ * entering every layer, and the rows after the last layer, into `buf` as
+ * [n_layer + 1][rows][d_model] in the activation dtype (rows = batch * L for a
+ * prefill, batch for a decode step); a call whose rows do not fit `bytes` is
+ * refused (LSSM_EINVAL).  buf = NULL turns it off.  Not combinable with
+ * lssm_engine_decode_graph. */
+int lssm_engine_set_trace(lssm_engine* e, void* buf, uint64_t bytes);
 int lssm_engine_state(lssm_engine* e, void** conv_state, void** ssd_state);
 /* conv_state: [n_layer, max_batch, xBC_dim, d_conv] act; ssd: [n_layer, max_batch, H, P, N] f32 */
 /* Layers of the last decode step (eager or captured) whose SSD step ran inside

@@ -29,6 +29,7 @@ LIB_PATH = os.path.join(_HERE, "liblssm_hip.so")
 F16, BF16, F32 = 0, 1, 2
 W_DENSE, W_Q4_B32, W_Q4_G64, W_Q8_G32 = 0, 6, 7, 8
 EPI_NONE, EPI_SILU, EPI_ADD = 0, 1, 2
+DEBUG_STALE_WAIT = 1   # lssm_ctx_set_debug: fused decode waits give up (failure-handling tests)
 
 
 class LssmError(RuntimeError):
@@ -109,6 +110,7 @@ _SIGS = {
     "lssm_commit_and_wait": ([_vp], _i),
     "lssm_batch_active": ([_vp], _i),
     "lssm_sync": ([_vp], _i),
+    "lssm_ctx_set_debug": ([_vp, _u32], _i),
     "lssm_library_loaded": ([], _i),
     "lssm_has_kernel": ([C.c_char_p], _i),
     "lssm_library_path": ([], C.c_char_p),
@@ -170,6 +172,7 @@ _SIGS = {
     "lssm_engine_decode": ([_vp, _vp, _u32, _vp], _i),
     "lssm_engine_decode_graph": ([_vp, _vp, _u32, _vp, _u32], _i),
     "lssm_engine_logits": ([_vp, C.POINTER(_vp)], _i),
+    "lssm_engine_set_trace": ([_vp, _vp, C.c_uint64], _i),
     "lssm_engine_state": ([_vp, C.POINTER(_vp), C.POINTER(_vp)], _i),
     "lssm_engine_fused_layers": ([_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)], _i),
     # .ssm files
@@ -257,6 +260,9 @@ class Ctx:
 
     def sync(self):
         check(lib.lssm_sync(self.h))
+
+    def set_debug(self, flags: int):
+        check(lib.lssm_ctx_set_debug(self.h, flags))
 
     def begin_batch(self):
         check(lib.lssm_begin_batch(self.h))

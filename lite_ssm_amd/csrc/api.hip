@@ -313,7 +313,7 @@ int lssm_inproj_ssd_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w
     a.xbc_act = nullptr;
     a.dt = nullptr;
     const SsdFuseArgs f{xfer, nullptr, tag, ssd_state, A_log, dt_bias, D_skip, y, d_head, d_state, n_groups,
-                        1e-6f, 1e6f};
+                        1e-6f, 1e6f, ctx->status, (ctx->debug & LSSM_DEBUG_STALE_WAIT) ? 1u : 0u};
     hipError_t e = hipSuccess;
     if (!launch_inproj_ssd_decode(ctx->stream, a, f, e))
         return set_error(LSSM_EINVAL, "inproj_ssd_decode: shape, format, alignment or grid not supported by the fused launch");
@@ -352,7 +352,7 @@ int lssm_mixer_decode(lssm_ctx* ctx, void* hidden, const void* norm_w, const voi
     a.xbc_act = nullptr;
     a.dt = nullptr;
     const SsdFuseArgs f{xfer, nullptr, tag, ssd_state, A_log, dt_bias, D_skip, nullptr, d_head, d_state, n_groups,
-                        1e-6f, 1e6f};
+                        1e-6f, 1e6f, ctx->status};
     const OutprojFuseArgs o{out_w, out_scales, mixer_norm_w, eps, hidden, reinterpret_cast<uint32_t*>(xfer + proj), d_model};
     hipError_t e = hipSuccess;
     if (!launch_layer_decode(ctx->stream, a, f, o, e))
@@ -365,8 +365,7 @@ int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out, 
                uint32_t d_model, uint32_t vocab, lssm_dtype act) {
     LSSM_CHECK_CTX(ctx);
     LSSM_REQUIRE(valid_act(act), "embed: unknown dtype");
-    
-    hipError_t e = launch_embed(ctx->stream, table, ids, out, n, d_model, vocab, act);
+    hipError_t e = launch_embed(ctx->stream, table, ids, out, n, d_model, vocab, act, ctx->status);
     if (e != hipSuccess) return set_error(LSSM_EDEVICE, "embed: %s", hipGetErrorString(e));
     return finish(ctx, "embed");
 }

@@ -28,15 +28,33 @@ int set_error(int code, const char* fmt, ...) {
 
 void clear_error() { g_err.clear(); }
 
+int sync_and_check(lssm_ctx* ctx, const char* what) {
+    hipError_t e = hipMemcpyAsync(ctx->status_host, ctx->status, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                  ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "%s failed: %s", what, hipGetErrorString(e));
+    const uint32_t st = *ctx->status_host;
+    if (st == 0) return LSSM_OK;
+    // clear for the next check (a plain copy: no memset node can end up in a
+    // captured graph from here, and the word is only written by kernels)
+    *ctx->status_host = 0;
+    e = hipMemcpyAsync(ctx->status, ctx->status_host, sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "%s failed: %s", what, hipGetErrorString(e));
+    // mamba2_model.cpp:129-131 throws std::out_of_range with this text
+    if (st & STATUS_BAD_TOKEN)
+        return set_error(LSSM_EINVAL, "Mamba2Model::embed: token_id out of range (%s)", what);
+    return set_error(LSSM_EDEVICE,
+                     "%s: a cross-workgroup wait timed out (the launch's workgroups were not all "
+                     "resident at once); the affected outputs are NaN and their state was not updated",
+                     what);
+}
+
 int finish(lssm_ctx* ctx, const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return set_error(LSSM_EDEVICE, "%s: launch failed: %s", what, hipGetErrorString(e));
-    if (!ctx->batch) {
-        e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess)
-            return set_error(LSSM_EDEVICE, "%s failed: %s", what, hipGetErrorString(e));
-    }
+    if (!ctx->batch) return sync_and_check(ctx, what);
     return LSSM_OK;
 }
 
@@ -82,6 +100,20 @@ int lssm_ctx_create(lssm_ctx** out, void* stream) {
         }
         c->own_stream = true;
     }
+    e = hipMalloc((void**)&c->status, 256);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&c->status_host, 256, hipHostMallocDefault);
+    if (e == hipSuccess) {
+        *c->status_host = 0;
+        e = hipMemcpyAsync(c->status, c->status_host, sizeof(uint32_t), hipMemcpyHostToDevice, c->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        if (c->status) (void)hipFree(c->status);
+        if (c->status_host) (void)hipHostFree(c->status_host);
+        if (c->own_stream) (void)hipStreamDestroy(c->stream);
+        delete c;
+        return set_error(LSSM_EDEVICE, "lssm_ctx_create: status word: %s", hipGetErrorString(e));
+    }
     *out = c;
     return LSSM_OK;
 }
@@ -91,6 +123,8 @@ int lssm_ctx_destroy(lssm_ctx* ctx) {
     if (!ctx) return LSSM_OK;
     // An uncommitted batch is dropped after the queued work drains (ops.mm:64-68).
     (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(ctx->status);
+    (void)hipHostFree(ctx->status_host);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return LSSM_OK;
@@ -116,21 +150,23 @@ int lssm_commit_and_wait(lssm_ctx* ctx) {
     if (!ctx->batch)
         return set_error(LSSM_ESTATE, "MetalOps: commit_and_wait without an active batch");
     ctx->batch = false;
-    hipError_t e = hipStreamSynchronize(ctx->stream);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return set_error(LSSM_EDEVICE, "HIP: forward batch failed: %s", hipGetErrorString(e));
-    e = hipGetLastError();
-    if (e != hipSuccess)
-        return set_error(LSSM_EDEVICE, "HIP: forward batch failed: %s", hipGetErrorString(e));
-    return LSSM_OK;
+    return sync_and_check(ctx, "HIP: forward batch");
 }
 
 int lssm_batch_active(lssm_ctx* ctx) { return (ctx && ctx->batch) ? 1 : 0; }
 
 int lssm_sync(lssm_ctx* ctx) {
     LSSM_CHECK_CTX(ctx);
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "lssm_sync: %s", hipGetErrorString(e));
+    return sync_and_check(ctx, "lssm_sync");
+}
+
+int lssm_ctx_set_debug(lssm_ctx* ctx, uint32_t flags) {
+    LSSM_CHECK_CTX(ctx);
+    LSSM_REQUIRE((flags & ~LSSM_DEBUG_STALE_WAIT) == 0, "lssm_ctx_set_debug: unknown flag");
+    ctx->debug = flags;
     return LSSM_OK;
 }
 

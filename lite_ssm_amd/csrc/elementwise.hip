@@ -349,12 +349,15 @@ __global__ void conv1d_seed_kernel(const T* __restrict__ xBC, uint32_t xs, T* __
     }
 }
 
-// mamba2_model.cpp:128-137 on device; out-of-range ids write zeros (the host
-// API rejects them before launch; this only guards the device read).
+// mamba2_model.cpp:128-137 on device.  The ids live in device memory, so the
+// range check of mamba2_model.cpp:129-131 happens here: an id outside
+// [0, vocab) gives a zero row (the table is never read out of bounds) and sets
+// STATUS_BAD_TOKEN in the context's status word, which the host turns into
+// the reference's out_of_range error at its next synchronisation point.
 template <typename T>
 __global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restrict__ ids,
                              T* __restrict__ out, uint32_t n, uint32_t d_model, uint32_t vocab,
-                             uint32_t* __restrict__ seq) {
+                             uint32_t* __restrict__ status, uint32_t* __restrict__ seq) {
     if (seq != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *seq += 1u;
     const size_t total = (size_t)n * d_model;
     for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
@@ -363,6 +366,7 @@ __global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restr
         const int32_t id = ids[i];
         const bool ok = id >= 0 && (uint32_t)id < vocab;
         out[e] = ok ? table[(size_t)id * d_model + c] : from_f<T>(0.0f);
+        if (!ok && c == 0) atomicOr(status, STATUS_BAD_TOKEN);
     }
 }
 
@@ -603,13 +607,13 @@ hipError_t launch_conv1d_keep_last(hipStream_t s, void* state, uint32_t n_window
 }
 
 hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, void* out, uint32_t n,
-                        uint32_t d_model, uint32_t vocab, int act, uint32_t* seq) {
+                        uint32_t d_model, uint32_t vocab, int act, uint32_t* status, uint32_t* seq) {
     if (n == 0) return hipSuccess;
     const size_t total = (size_t)n * d_model;
     const unsigned blocks = (unsigned)((total + NT - 1) / NT < 65536 ? (total + NT - 1) / NT : 65536);
     LSSM_DISPATCH_ACT(act, T,
                       embed_kernel<T><<<blocks, NT, 0, s>>>((const T*)table, ids, (T*)out, n,
-                                                            d_model, vocab, seq));
+                                                            d_model, vocab, status, seq));
     return hipGetLastError();
 }
 

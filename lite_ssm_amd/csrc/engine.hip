@@ -57,6 +57,15 @@ struct lssm_engine {
     void* d_g = nullptr;
     void* d_gn = nullptr;      // also the packed x rows of the MFMA decode GEMV (launch_mma_pack)
     void* logits = nullptr;
+    // short fp16 prefills (1 < L <= 16, dense fp16 weights): the fused in_proj
+    // + conv + SiLU split's outputs [max_batch * 16, .] (mamba2_block.cpp:98)
+    void* f_z = nullptr;
+    void* f_x = nullptr;
+    void* f_B = nullptr;
+    void* f_C = nullptr;
+    void* f_dt = nullptr;
+    void* f_xbc = nullptr;
+    bool short_fused() const { return act == LSSM_F16 && wfmt == LSSM_W_DENSE; }
     void* conv_state = nullptr;
     float* ssd_state = nullptr;
     void* argmax_scratch = nullptr;
@@ -79,6 +88,17 @@ struct lssm_engine {
     mutable uint32_t fused_layers = 0;   // of the last decode step issued: SSD in the in_proj launch
     mutable uint32_t mixer_layers = 0;   //   the whole mixer (+ out_proj) in one launch
     size_t xfer_words() const { return (size_t)proj + d_inner; }   // per layer: [z|xBC|dt] + gated y
+
+    // parity hook (lssm_engine_set_trace): hidden rows entering each layer
+    // and after the last one, [n_layer + 1][rows][d_model], or null
+    void* trace = nullptr;
+    size_t trace_cap = 0;
+    size_t trace_bytes(uint32_t rows) const { return (size_t)(cfg.n_layer + 1) * rows * d_model * es; }
+    hipError_t trace_rows(uint32_t slot, const void* h, uint32_t rows) const {
+        if (!trace) return hipSuccess;
+        const size_t n = (size_t)rows * d_model * es;
+        return hipMemcpyAsync((char*)trace + (size_t)slot * n, h, n, hipMemcpyDeviceToDevice, st());
+    }
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -143,7 +163,7 @@ struct lssm_engine {
     hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
         // the step tag advances on batch-1 steps only, the ones that use the
         // tagged words: every use then finds the previous use's tag, minus one
-        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act,
+        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act, ctx->status,
                                     fuse_ssd && B == 1 ? seq : nullptr);
         // fused RMSNorm + linear kernels: the VALU GEMV up to 4 rows, the MFMA
         // GEMV for decode batches of the shapes it takes
@@ -160,7 +180,10 @@ struct lssm_engine {
                               gemv_mma_takes(B, d_model, d_inner, wfmt, act);
         fused_layers = 0;
         mixer_layers = 0;
+        if (e == hipSuccess) e = trace_rows(0, d_hidden, B);
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
+            if (li > 0) e = trace_rows(li, d_hidden, B);
+            if (e != hipSuccess) break;
             const lssm_layer_weights& w = layers[li];
             char* cs = conv_layer(li);
             bool ssd_done = false;   // the SSD step ran inside the in_proj launch
@@ -182,7 +205,7 @@ struct lssm_engine {
                 if (B == 1 && fuse_ssd) {
                     uint64_t* lx = xfer + (size_t)li * xfer_words();
                     const SsdFuseArgs f{lx, seq, 0u, ssd_layer(li), w.A_log, w.dt_bias, w.D,
-                                        d_g, P, N, G, DT_MIN, DT_MAX};
+                                        d_g, P, N, G, DT_MIN, DT_MAX, ctx->status};
                     if (fused_out && fuse_mixer) {
                         const OutprojFuseArgs o{w.out_proj_w, w.out_proj_s, w.mixer_norm_w, RMS_EPS, d_hidden,
                                                 reinterpret_cast<uint32_t*>(lx + proj), d_model};
@@ -236,6 +259,7 @@ struct lssm_engine {
                                B, d_model, d_inner, wfmt, LSSM_EPI_ADD);
             }
         }
+        if (e == hipSuccess) e = trace_rows(cfg.n_layer, d_hidden, B);
         if (e == hipSuccess) e = logits_argmax(d_hidden, d_model, B, next);
         return e;
     }
@@ -250,51 +274,92 @@ struct lssm_engine {
             return e;
         }
         const uint32_t R = B * L;
-        hipError_t e = launch_embed(st(), embed, ids, hidden, R, d_model, vocab, act);
+        hipError_t e = launch_embed(st(), embed, ids, hidden, R, d_model, vocab, act, ctx->status);
         const uint32_t ck = cfg.chunk_size < L ? (cfg.chunk_size < 64 ? cfg.chunk_size : 64)
                                                : (L < 64 ? L : 64);
+        // mamba2_block.cpp:97-98: a short prefill of fp16 weights takes the
+        // fused in_proj + conv + SiLU split (its conv reads the unrounded
+        // projection, so it rounds differently from the chain below)
+        const bool fused = short_fused() && L > 1 && L <= 16;
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
-            e = launch_rmsnorm(st(), hidden, d_model, w.norm_w, normed, d_model, R, d_model, RMS_EPS, act);
-            if (e == hipSuccess) {
+            e = trace_rows(li, hidden, R);
+            if (e == hipSuccess)
+                e = launch_rmsnorm(st(), hidden, d_model, w.norm_w, normed, d_model, R, d_model, RMS_EPS, act);
+            if (e == hipSuccess && !fused) {
                 GemmArgs g{normed, d_model, w.in_proj_w, w.in_proj_s, projb, proj, nullptr, R, proj,
                            d_model, wfmt, act, LSSM_EPI_NONE, 1};
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
             }
-            const char* xbc_pre = (const char*)projb + (size_t)d_inner * es;
-            if (e == hipSuccess)
-                e = launch_conv1d(st(), xbc_pre, proj, w.conv1d_w, w.conv1d_b, xbc_act, xbc, B, L, xbc,
-                                  K, act, true);
-            if (e == hipSuccess) e = launch_conv1d_seed(st(), xbc_pre, proj, conv_layer(li), B, L, xbc, K, act);
-            if (e == hipSuccess) {
-                SsdArgs s{xbc_act, xbc, (char*)xbc_act + (size_t)d_inner * es, xbc,
-                          (char*)xbc_act + (size_t)(d_inner + GN) * es, xbc,
-                          (char*)projb + (size_t)(d_inner + xbc) * es, proj, w.dt_bias, w.A_log, w.D,
-                          ys, d_inner, ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act,
-                          nullptr, 0};
-                e = launch_ssd_chunked(st(), s);
+            if (e != hipSuccess) break;
+            if (fused) {
+                e = short_prefill_mixer(li, B, L, ck);
+            } else {
+                const char* xbc_pre = (const char*)projb + (size_t)d_inner * es;
+                e = launch_conv1d(st(), xbc_pre, proj, w.conv1d_w, w.conv1d_b, xbc_act, xbc, B, L, xbc, K,
+                                  act, true);
+                if (e == hipSuccess)
+                    e = launch_conv1d_seed(st(), xbc_pre, proj, conv_layer(li), B, L, xbc, K, act);
+                if (e == hipSuccess) {
+                    SsdArgs s{xbc_act, xbc, (char*)xbc_act + (size_t)d_inner * es, xbc,
+                              (char*)xbc_act + (size_t)(d_inner + GN) * es, xbc,
+                              (char*)projb + (size_t)(d_inner + xbc) * es, proj, w.dt_bias, w.A_log, w.D,
+                              ys, d_inner, ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act,
+                              nullptr, 0};
+                    e = launch_ssd_chunked(st(), s);
+                }
+                if (e == hipSuccess)
+                    e = launch_gated_rmsnorm(st(), projb, proj, ys, d_inner, w.mixer_norm_w, gn, R, d_inner,
+                                             RMS_EPS, act);
             }
-            if (e == hipSuccess)
-                e = launch_gated_rmsnorm(st(), projb, proj, ys, d_inner, w.mixer_norm_w, gn, R, d_inner,
-                                         RMS_EPS, act);
             if (e == hipSuccess) {
                 GemmArgs g{gn, d_inner, w.out_proj_w, w.out_proj_s, hidden, d_model, hidden, R, d_model,
                            d_inner, wfmt, act, LSSM_EPI_ADD, 1};
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
             }
         }
+        if (e == hipSuccess) e = trace_rows(cfg.n_layer, hidden, R);
         // last position of each sequence: rows (b*L + L-1), stride L*d_model
         if (e == hipSuccess)
             e = logits_argmax((const char*)hidden + (size_t)(L - 1) * d_model * es, L * d_model, B, next);
         return e;
     }
 
+    // The mixer of layer li for a short fp16 prefill, per sequence as the
+    // reference's batch-1 model (mamba2_block.cpp:130-148, then the seed from
+    // the pre-conv projection, the chunked scan and the gated norm over the
+    // fused op's outputs).  normed holds the layer's normalised input rows.
+    hipError_t short_prefill_mixer(uint32_t li, uint32_t B, uint32_t L, uint32_t ck) const {
+        const lssm_layer_weights& w = layers[li];
+        const lssm_fused_inproj_dims fd{L, d_model, d_inner, N, G, H, K, proj};
+        hipError_t e = hipSuccess;
+        for (uint32_t b = 0; b < B && e == hipSuccess; ++b) {
+            const size_t r0 = (size_t)b * L;
+            e = launch_inproj_fused(st(), (const char*)normed + r0 * d_model * es, w.in_proj_w, w.conv1d_w,
+                                    w.conv1d_b, (char*)f_z + r0 * d_inner * es, (char*)f_x + r0 * d_inner * es,
+                                    (char*)f_B + r0 * GN * es, (char*)f_C + r0 * GN * es,
+                                    (char*)f_dt + r0 * H * es, (char*)f_xbc + r0 * xbc * es, fd);
+        }
+        if (e == hipSuccess) e = launch_conv1d_seed(st(), f_xbc, xbc, conv_layer(li), B, L, xbc, K, act);
+        if (e == hipSuccess) {
+            SsdArgs s{f_x, d_inner, f_B, GN, f_C, GN, f_dt, H, w.dt_bias, w.A_log, w.D, ys, d_inner,
+                      ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act, nullptr, 0};
+            e = launch_ssd_chunked(st(), s);
+        }
+        if (e == hipSuccess)
+            e = launch_gated_rmsnorm(st(), f_z, d_inner, ys, d_inner, w.mixer_norm_w, gn, B * L, d_inner, RMS_EPS,
+                                     act);
+        return e;
+    }
+
     hipError_t decode_layers_for_prefill1(const int32_t* ids, uint32_t B) const {
         // same kernels as a decode step without logits, then the 1-row seed
-        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act);
+        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act, ctx->status);
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
-            e = launch_rmsnorm(st(), d_hidden, d_model, w.norm_w, d_normed, d_model, B, d_model, RMS_EPS, act);
+            e = trace_rows(li, d_hidden, B);
+            if (e == hipSuccess)
+                e = launch_rmsnorm(st(), d_hidden, d_model, w.norm_w, d_normed, d_model, B, d_model, RMS_EPS, act);
             if (e == hipSuccess)
                 e = linear(d_normed, d_model, w.in_proj_w, w.in_proj_s, d_proj, proj, nullptr, B, proj,
                            d_model, wfmt, LSSM_EPI_NONE);
@@ -316,6 +381,7 @@ struct lssm_engine {
                 e = linear(d_gn, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden, B,
                            d_model, d_inner, wfmt, LSSM_EPI_ADD);
         }
+        if (e == hipSuccess) e = trace_rows(cfg.n_layer, d_hidden, B);
         return e;
     }
 };
@@ -412,6 +478,15 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A(&e->conv_state, (size_t)cfg->n_layer * max_batch * e->xbc * e->K * es);
     A((void**)&e->ssd_state, (size_t)cfg->n_layer * max_batch * e->H * e->P * e->N * sizeof(float));
     A(&e->argmax_scratch, (size_t)max_batch * 128 * 8);
+    if (e->short_fused()) {
+        const size_t R16 = (size_t)max_batch * 16;
+        A(&e->f_z, R16 * d_inner * es);
+        A(&e->f_x, R16 * d_inner * es);
+        A(&e->f_B, R16 * e->GN * es);
+        A(&e->f_C, R16 * e->GN * es);
+        A(&e->f_dt, R16 * e->H * es);
+        A(&e->f_xbc, R16 * e->xbc * es);
+    }
     const size_t xfer_bytes = (size_t)cfg->n_layer * e->xfer_words() * sizeof(uint64_t);
     A((void**)&e->xfer, xfer_bytes);
     A((void**)&e->seq, 256);
@@ -458,6 +533,8 @@ int lssm_engine_prefill(lssm_engine* e, const int32_t* ids, uint32_t batch, uint
     LSSM_REQUIRE(L <= e->max_seq, "forward_prefill: L exceeds workspace max_seq_len"); // :301-303
     LSSM_REQUIRE(batch >= 1 && batch <= e->max_batch, "forward_prefill: batch out of range");
     LSSM_REQUIRE(ids && next_ids, "forward_prefill: null ids");
+    LSSM_REQUIRE(!e->trace || e->trace_bytes(L == 1 ? batch : batch * L) <= e->trace_cap,
+                 "engine_prefill: trace buffer too small");
     return engine_finish(e, e->prefill(ids, batch, L, next_ids), "engine_prefill");
 }
 
@@ -465,12 +542,22 @@ int lssm_engine_decode(lssm_engine* e, const int32_t* ids, uint32_t batch, int32
     if (int rc = check_engine(e)) return rc;
     LSSM_REQUIRE(batch >= 1 && batch <= e->max_batch, "forward_step: batch out of range");
     LSSM_REQUIRE(ids && next_ids, "forward_step: null ids");
+    LSSM_REQUIRE(!e->trace || e->trace_bytes(batch) <= e->trace_cap, "engine_decode: trace buffer too small");
     return engine_finish(e, e->decode(ids, batch, next_ids), "engine_decode");
+}
+
+int lssm_engine_set_trace(lssm_engine* e, void* buf, uint64_t bytes) {
+    if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(!buf || bytes > 0, "engine_set_trace: empty buffer");
+    e->trace = buf;
+    e->trace_cap = buf ? (size_t)bytes : 0;
+    return LSSM_OK;
 }
 
 int lssm_engine_decode_graph(lssm_engine* e, const int32_t* ids, uint32_t batch, int32_t* next_ids,
                              uint32_t steps) {
     if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(!e->trace, "engine_decode_graph: not with a trace buffer set (lssm_engine_set_trace)");
     LSSM_REQUIRE(batch >= 1 && batch <= e->max_batch, "forward_step: batch out of range");
     LSSM_REQUIRE(ids && next_ids, "forward_step: null ids");
     hipStream_t s = e->ctx->stream;

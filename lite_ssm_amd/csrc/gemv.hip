@@ -52,8 +52,10 @@ namespace {
 // C of the head's group, x and z of its columns, dt of the head), which other
 // blocks of the same launch store.  The launcher fuses only when every block
 // of the launch is resident at once (at most one block per CU), so every
-// awaited word gets written; the wait is bounded all the same, and a column
-// whose words never arrive gets a NaN output.
+// awaited word gets written; the wait is bounded all the same: an item whose
+// words do not all arrive leaves its state slice as it was, writes NaN
+// outputs and sets STATUS_WAIT_TIMEOUT in the context's status word, which
+// the host reports as an error at its next synchronisation point.
 template <typename T> struct EpiInprojSsd {
     static constexpr bool kNormOptional = false;
     static constexpr bool kTail = true;
@@ -77,6 +79,9 @@ template <typename T> struct EpiInprojSsd {
                                                           //   value | (tag mod 2^16) << 16
     uint32_t P, G, items;                                 // items = H * P / IP
     float dt_min, dt_max;
+    uint32_t* status;                                     // STATUS_WAIT_TIMEOUT on a failed wait
+    uint32_t wait_skew;                                   // 0; 1 = wait for a tag nobody publishes
+                                                          // (the failure-handling test's switch)
     using Pre = typename EpiInproj<T>::Pre;
     struct Early {
         f32x4 s[F];
@@ -94,6 +99,7 @@ template <typename T> struct EpiInprojSsd {
         pin_arg(D);
         pin_arg(P);
         pin_arg(items);
+        pin_arg(status);
     }
     __device__ __forceinline__ Pre prefetch(int m, uint32_t n) const { return in.prefetch(m, n); }
     __device__ __forceinline__ void operator()(int m, uint32_t n, float acc, const Pre& p) const {
@@ -123,6 +129,7 @@ template <typename T> struct EpiInprojSsd {
         const uint32_t d_inner = in.d_inner, H = in.H, GN = G * NN, ipp = P / IP;
         const uint32_t h = it / ipp, p0 = (it % ipp) * IP, g = h / (H / G);
         __syncthreads();                                  // a previous item's words read
+        int late = 0;                                     // a word of this thread never arrived
         for (uint32_t t = threadIdx.x; t < NWD; t += blockDim.x) {
             uint32_t idx;
             if (t < NN) idx = 2 * d_inner + g * NN + t;                              // B
@@ -133,9 +140,12 @@ template <typename T> struct EpiInprojSsd {
             uint64_t v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             for (uint32_t n = 0; (uint32_t)(v >> 32) != tag && n < SPIN; ++n)
                 v = __hip_atomic_load(xfer + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            late |= (uint32_t)(v >> 32) != tag;
             wv[t] = (uint32_t)(v >> 32) == tag ? (uint32_t)v : QNAN;
         }
-        __syncthreads();
+        // the state slice is stored only when every word of the item arrived
+        const bool timed_out = __syncthreads_or(late) != 0;
+        if (timed_out && threadIdx.x == 0) atomicOr(status, STATUS_WAIT_TIMEOUT);
         if (threadIdx.x >= IP * NV) return;               // wave-uniform; no barrier follows
         const uint32_t lr = threadIdx.x % NV, pl = threadIdx.x / NV;
         f32x4* S = reinterpret_cast<f32x4*>(state + ((size_t)h * P + p0 + pl) * NN);
@@ -158,7 +168,7 @@ template <typename T> struct EpiInprojSsd {
             t.y = fmaf(decay, t.y, dt * b1 * xv);
             t.z = fmaf(decay, t.z, dt * b2 * xv);
             t.w = fmaf(decay, t.w, dt * b3 * xv);
-            S[lr + NV * f] = t;
+            if (!timed_out) S[lr + NV * f] = t;
             ys += fmaf(c3, t.w, fmaf(c2, t.z, fmaf(c0, t.x, c1 * t.y)));
         }
         ys = group_sum<NV>(ys);
@@ -172,7 +182,7 @@ template <typename T> struct EpiInprojSsd {
         }
     }
     __device__ __forceinline__ void tail(const Early& e) const {
-        const uint32_t tag = seq ? *seq : tag0;
+        const uint32_t tag = (seq ? *seq : tag0) + wait_skew;
         if (blockIdx.x < items) item(blockIdx.x, e.s, e.alr, e.dbr, e.dr, tag);
         // items beyond one per workgroup (not with the engine's shapes): state loaded here
         const uint32_t ipp = P / IP;
@@ -308,11 +318,14 @@ template <typename T, int FMT, int LPR2, int CPL2> struct EpiLayer {
                         x[r] = __hip_atomic_load(ssd.yx + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
+            bool late = false;
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 const uint32_t k = k0 + threadIdx.x + blockDim.x * r;
                 if (k < K2) ybuf[k] = (uint16_t)((x[r] >> 16) == tag16 ? (x[r] & 0xFFFFu) : QNAN);
+                late |= k < K2 && (x[r] >> 16) != tag16;
             }
+            if (late) atomicOr(ssd.status, STATUS_WAIT_TIMEOUT);
         }
         __syncthreads();
         uint4 xo[OCT2];
@@ -1115,6 +1128,8 @@ template <typename T> EpiInprojSsd<T> make_ssd_epi(const InprojDecodeArgs& a, co
     e.items = a.H * (f.P / EpiInprojSsd<T>::IP);
     e.dt_min = f.dt_min;
     e.dt_max = f.dt_max;
+    e.status = f.status;
+    e.wait_skew = f.wait_skew;
     return e;
 }
 }  // namespace

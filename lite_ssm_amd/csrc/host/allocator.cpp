@@ -1,9 +1,9 @@
-// allocator.cpp — MmapFile / DeviceBuffer / UnifiedBuffer for the HIP backend.
+// allocator.cpp — DeviceBuffer / UnifiedBuffer for the HIP backend.
 //
 // Interface: include/lite_ssm/allocator.hpp (reference include/lite_ssm/allocator.hpp).
-// MmapFile follows the reference's src/core/allocator.cpp:31-64 (open, fstat,
-// page-rounded PROT_READ/MAP_PRIVATE mapping, same error messages).  The
-// Metal bridge (src/backend/metal/metal_buffer.mm) becomes:
+// MmapFile is not part of the backend: it is portable POSIX code and stays the
+// reference's own (src/core/allocator.cpp:31-99), linked beside this library.
+// The Metal bridge (src/backend/metal/metal_buffer.mm) becomes:
 //   DeviceBuffer  -> lssm_malloc_host: pinned, coherent host memory mapped
 //                    into the GPU, so the model layer's contents() reads and
 //                    writes (embedding rows in, logits out) keep working with no
@@ -18,84 +18,19 @@
 #include "lite_ssm/allocator.hpp"
 #include "lssm.h"
 
-#include <cerrno>
 #include <cstring>
-#include <fcntl.h>
 #include <stdexcept>
 #include <string>
-#include <sys/mman.h>
-#include <sys/stat.h>
-#include <unistd.h>
 
 namespace lite_ssm {
 
 namespace {
-
-std::size_t page_size_bytes() {
-    long ps = ::sysconf(_SC_PAGESIZE);
-    return ps > 0 ? static_cast<std::size_t>(ps) : 4096;
-}
 
 [[noreturn]] void throw_lssm(const char* what) {
     throw std::runtime_error(std::string(what) + ": " + lssm_last_error());
 }
 
 }  // namespace
-
-// ---------------------------------------------------------------------------
-// MmapFile
-// ---------------------------------------------------------------------------
-MmapFile::MmapFile(const std::string& path) {
-    const int fd = ::open(path.c_str(), O_RDONLY);
-    if (fd < 0)
-        throw std::runtime_error("MmapFile: open('" + path + "') failed: " + std::strerror(errno));
-    struct stat st {};
-    if (::fstat(fd, &st) != 0) {
-        const int err = errno;
-        ::close(fd);
-        throw std::runtime_error("MmapFile: fstat failed: " + std::string(std::strerror(err)));
-    }
-    if (st.st_size <= 0) {
-        ::close(fd);
-        throw std::runtime_error("MmapFile: empty or invalid file '" + path + "'");
-    }
-    const std::size_t size  = static_cast<std::size_t>(st.st_size);
-    const std::size_t page  = page_size_bytes();
-    const std::size_t total = (size + page - 1) / page * page;
-    void* p = ::mmap(nullptr, total, PROT_READ, MAP_PRIVATE, fd, 0);
-    ::close(fd);
-    if (p == MAP_FAILED)
-        throw std::runtime_error("MmapFile: mmap failed: " + std::string(std::strerror(errno)));
-    ptr_         = p;
-    file_size_   = size;
-    mapped_size_ = total;
-}
-
-MmapFile::~MmapFile() { reset_(); }
-
-MmapFile::MmapFile(MmapFile&& o) noexcept
-    : ptr_(o.ptr_), file_size_(o.file_size_), mapped_size_(o.mapped_size_) {
-    o.ptr_ = nullptr;
-    o.file_size_ = o.mapped_size_ = 0;
-}
-
-MmapFile& MmapFile::operator=(MmapFile&& o) noexcept {
-    if (this != &o) {
-        reset_();
-        ptr_         = o.ptr_;
-        file_size_   = o.file_size_;
-        mapped_size_ = o.mapped_size_;
-        o.ptr_ = nullptr;
-        o.file_size_ = o.mapped_size_ = 0;
-    }
-    return *this;
-}
-
-void MmapFile::reset_() noexcept {
-    if (ptr_) ::munmap(ptr_, mapped_size_);
-    ptr_ = nullptr;
-    file_size_ = mapped_size_ = 0;
-}
 
 // ---------------------------------------------------------------------------
 // DeviceBuffer

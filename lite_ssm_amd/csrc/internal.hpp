@@ -20,6 +20,12 @@ struct lssm_ctx {
     bool own_stream = false;
     bool batch = false;
     int device = 0;
+    // Device status word (LSSM_STATUS_* bits, OR-ed by kernels that detect a
+    // condition they cannot report otherwise) and its pinned host mirror; read
+    // and cleared at every synchronisation point of the context.
+    uint32_t* status = nullptr;
+    uint32_t* status_host = nullptr;
+    uint32_t debug = 0;      // LSSM_DEBUG_* switches (lssm_ctx_set_debug)
 };
 
 namespace lssm {
@@ -31,9 +37,16 @@ uint32_t num_cus();
 int set_error(int code, const char* fmt, ...);
 void clear_error();
 
+// Bits of lssm_ctx::status.
+constexpr uint32_t STATUS_BAD_TOKEN = 1u;      // a token id outside [0, vocab) reached the embedding
+constexpr uint32_t STATUS_WAIT_TIMEOUT = 2u;   // a cross-workgroup wait gave up (not co-resident)
+
 // After enqueueing an op: report launch errors; outside a batch, also wait and
-// report asynchronous kernel failures.
+// report asynchronous kernel failures and the device status word.
 int finish(lssm_ctx* ctx, const char* what);
+// Wait for the context's stream; report a HIP error or a status bit set by a
+// kernel since the last check (and clear it).
+int sync_and_check(lssm_ctx* ctx, const char* what);
 
 // Dynamic LDS of the GEMV x staging (fp32 rows); static + dynamic stays <= 64 KiB.
 constexpr size_t GEMV_LDS_BYTES = 60 * 1024;
@@ -88,8 +101,10 @@ hipError_t launch_conv1d_seed(hipStream_t s, const void* xBC, uint32_t x_stride,
                               uint32_t B, uint32_t L, uint32_t D, uint32_t K, int act);
 // seq (optional): a step counter the kernel advances by one (the tag of the
 // fused decode launch's words).
+// An id outside [0, vocab) gives a zero row and sets STATUS_BAD_TOKEN in *status.
 hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, void* out,
-                        uint32_t n, uint32_t d_model, uint32_t vocab, int act, uint32_t* seq = nullptr);
+                        uint32_t n, uint32_t d_model, uint32_t vocab, int act, uint32_t* status,
+                        uint32_t* seq = nullptr);
 hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32_t rows,
                          uint32_t vocab, int act, void* scratch);
 
@@ -193,6 +208,10 @@ struct SsdFuseArgs {
     void* y;                 // [d_inner]
     uint32_t P, N, G;
     float dt_min, dt_max;
+    uint32_t* status;        // STATUS_WAIT_TIMEOUT when a wait gives up (that item's
+                             // state is then left as it was, its outputs NaN)
+    uint32_t wait_skew = 0;  // 1: the SSD items wait for a tag that is never published,
+                             // so every bounded wait gives up (LSSM_DEBUG_STALE_WAIT)
 };
 bool launch_inproj_ssd_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseArgs& f, hipError_t& err);
 // The whole mixer of a layer at batch 1 in one launch: launch_inproj_ssd_decode

@@ -114,7 +114,10 @@ class DeviceModel:
     """Random-init Mamba-2 weights resident in HBM (one GPU)."""
 
     def __init__(self, sh: Shape, act: int = BF16, wfmt: int = W_Q4_G64, seed: int = 0,
-                 device: str = "cuda", std: float = 0.02):
+                 device: str = "cuda", std: float = 0.02, embed_std: float | None = None):
+        """Random init: linears ~ N(0, std), embeddings ~ N(0, embed_std or std).
+        A larger embed_std (the lm_head is tied) spreads the logits, so the
+        greedy choice is rarely a near-tie at the logits' fp16 resolution."""
         self.shape, self.act, self.wfmt, self.device = sh, act, wfmt, device
         dt = TORCH_DTYPE[act]
         g = torch.Generator(device=device)
@@ -134,7 +137,7 @@ class DeviceModel:
             return quantize(w, wfmt)
 
         H = sh.n_heads
-        self.embed = act_t(randn(sh.vocab_size, sh.d_model, scale=std))
+        self.embed = act_t(randn(sh.vocab_size, sh.d_model, scale=std if embed_std is None else embed_std))
         self.norm_f = act_t(randn(sh.d_model, scale=0.1, mean=1.0))
         self.layers = []
         for _ in range(sh.n_layer):
@@ -246,6 +249,16 @@ class Engine:
                           device=self.model.device)
         check(lib.lssm_memcpy_d2d(self.ctx.h, out.data_ptr(), p.value, out.numel() * out.element_size()))
         return out
+
+    def set_trace(self, buf):
+        """Parity hook: every later prefill / decode writes the hidden rows
+        entering each layer (and after the last) into `buf` (a device tensor of
+        at least (n_layer + 1) * rows * d_model activation elements), or None."""
+        if buf is None:
+            check(lib.lssm_engine_set_trace(self.h, None, 0))
+        else:
+            check(lib.lssm_engine_set_trace(self.h, buf.data_ptr(), buf.numel() * buf.element_size()))
+        self._trace = buf
 
     def fused_layers(self):
         """(layers of the last decode step whose SSD step ran inside the in_proj

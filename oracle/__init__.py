@@ -93,6 +93,8 @@ _SIGS = {
     "orc_argmax": ([_vp, _vp, _u32, _u32, _i], None),
     "orc_model_prefill": ([C.POINTER(_Model), _vp, _vp, _vp, _u32, _u32, _vp], None),
     "orc_model_decode": ([C.POINTER(_Model), _vp, _vp, _vp, _u32, _vp], None),
+    "orc_model_block": ([C.POINTER(_Model), _u32, _vp, _vp, _vp, _u32, _u32, _i], None),
+    "orc_model_logits": ([C.POINTER(_Model), _vp, _u32, _vp], None),
     "orc_num_threads": ([], _i),
     "orc_set_num_threads": ([_i], None),
 }
@@ -310,6 +312,22 @@ class Model:
         logits = np.empty((batch, self.cfg["vocab_size"]), dtype=act_np_dtype(self.act))
         _L.orc_model_prefill(C.byref(self._m), _ptr(conv), _ptr(ssd), _ptr(ids), batch, L, _ptr(logits))
         return logits
+
+    def block(self, li, hidden, conv, ssd, batch, L, decode):
+        """run_block of layer li on `hidden` ([batch * L, d_model] act bits,
+        updated in place); conv / ssd are new_state(batch) arrays."""
+        assert hidden.flags["C_CONTIGUOUS"] and hidden.shape == (batch * L, self.cfg["d_model"])
+        _L.orc_model_block(C.byref(self._m), li, _ptr(hidden), _ptr(conv), _ptr(ssd), batch, L,
+                           1 if decode else 0)
+        return hidden
+
+    def logits(self, hidden_rows):
+        """norm_f + lm_head of hidden rows [rows, d_model] -> logits [rows, vocab]."""
+        hidden_rows = np.ascontiguousarray(hidden_rows)
+        rows = hidden_rows.shape[0]
+        out = np.empty((rows, self.cfg["vocab_size"]), dtype=act_np_dtype(self.act))
+        _L.orc_model_logits(C.byref(self._m), _ptr(hidden_rows), rows, _ptr(out))
+        return out
 
     def decode(self, conv, ssd, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

@@ -175,9 +175,22 @@ static void deq_row(const void* w, const void* s, float* out, uint32_t n, uint32
     size_t row_bytes = (wfmt == LSSM_W_Q8_G32) ? K : K / 2;
     uint32_t G = (uint32_t)orc_wfmt_group(wfmt);
     uint32_t gpr = K / G;
-    for (uint32_t k = 0; k < K; ++k) {
-        float sc = orc_h2f(scales[(size_t)n * gpr + k / G]);
-        out[k] = (float)q_at(packed, row_bytes, n, k, wfmt) * sc;
+    const uint8_t* row = packed + (size_t)n * row_bytes;
+    for (uint32_t g = 0; g < gpr; ++g) {
+        const float sc = orc_h2f(scales[(size_t)n * gpr + g]);
+        float* o = out + (size_t)g * G;
+        if (wfmt == LSSM_W_Q8_G32) {
+            for (uint32_t i = 0; i < G; ++i) o[i] = (float)(int8_t)row[(size_t)g * G + i] * sc;
+        } else {
+            /* linear.metal:47-61: low nibble = even k, two's complement 4-bit */
+            const uint8_t* b = row + (size_t)g * G / 2;
+            for (uint32_t i = 0; i < G / 2; ++i) {
+                /* sign-extend each nibble: shift it to the top of a signed byte */
+                const int lo = (int8_t)(uint8_t)(b[i] << 4) >> 4, hi = (int8_t)b[i] >> 4;
+                o[2 * i] = (float)lo * sc;
+                o[2 * i + 1] = (float)hi * sc;
+            }
+        }
     }
 }
 
@@ -250,6 +263,52 @@ void orc_rmsnorm(const void* x, const void* w, void* y, uint32_t rows, uint32_t 
     }
 }
 
+/* Sum of a[k] * b[k] in double.  Sixteen independent partial sums (the order
+ * in which double additions happen is immaterial at every tolerance the
+ * oracle is used with) keep the loop vectorised instead of latency-bound. */
+typedef double v4d __attribute__((vector_size(32)));
+static inline v4d ld4(const double* p) {
+    v4d v;
+    memcpy(&v, p, sizeof(v));
+    return v;
+}
+static inline double hsum4(v4d v) { return (v[0] + v[1]) + (v[2] + v[3]); }
+
+/* Sums of w[k] * x_r[k] in double for rows x_0..x_3 of x (row stride K), with
+ * independent partial sums: the order of double additions is immaterial at
+ * every tolerance the oracle is used with, and this keeps the loop vectorised
+ * with the weight row loaded once for four rows. */
+static void dot4_f64(const double* w, const double* x, uint32_t K, double* out) {
+    const double *x0 = x, *x1 = x + K, *x2 = x + 2 * (size_t)K, *x3 = x + 3 * (size_t)K;
+    v4d a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0, b0 = a0, b1 = a0, b2 = a0, b3 = a0;
+    uint32_t k = 0;
+    for (; k + 8 <= K; k += 8) {
+        const v4d w0 = ld4(w + k), w1 = ld4(w + k + 4);
+        a0 += w0 * ld4(x0 + k); b0 += w1 * ld4(x0 + k + 4);
+        a1 += w0 * ld4(x1 + k); b1 += w1 * ld4(x1 + k + 4);
+        a2 += w0 * ld4(x2 + k); b2 += w1 * ld4(x2 + k + 4);
+        a3 += w0 * ld4(x3 + k); b3 += w1 * ld4(x3 + k + 4);
+    }
+    out[0] = hsum4(a0 + b0); out[1] = hsum4(a1 + b1); out[2] = hsum4(a2 + b2); out[3] = hsum4(a3 + b3);
+    for (; k < K; ++k) {
+        out[0] += w[k] * x0[k]; out[1] += w[k] * x1[k]; out[2] += w[k] * x2[k]; out[3] += w[k] * x3[k];
+    }
+}
+
+static double dot1_f64(const double* w, const double* x, uint32_t K) {
+    v4d a = {0, 0, 0, 0}, b = a, c = a, d = a;
+    uint32_t k = 0;
+    for (; k + 16 <= K; k += 16) {
+        a += ld4(w + k) * ld4(x + k);
+        b += ld4(w + k + 4) * ld4(x + k + 4);
+        c += ld4(w + k + 8) * ld4(x + k + 8);
+        d += ld4(w + k + 12) * ld4(x + k + 12);
+    }
+    double t = hsum4((a + b) + (c + d));
+    for (; k < K; ++k) t += w[k] * x[k];
+    return t;
+}
+
 /* linear.metal:82-109 (f16 GEMV), 440-474 (int4 GEMV: exact fp32 dequant),
  * 253-343 / 492-574 (GEMMs: int4 dequant rounded to half, linear.metal:538),
  * 113-138 / 347-423 (SiLU epilogue), activations.metal:24-32 (residual add).
@@ -259,22 +318,24 @@ void orc_linear(const void* x, uint32_t x_stride, const void* w, const void* s, 
                 int wfmt, int act, int epi, int round_dequant) {
     if (x_stride == 0) x_stride = K;
     if (y_stride == 0) y_stride = N;
-    float* xf = (float*)malloc(sizeof(float) * (size_t)M * K);
+    double* xd = (double*)malloc(sizeof(double) * (size_t)M * K);
     for (uint32_t m = 0; m < M; ++m)
-        for (uint32_t k = 0; k < K; ++k) xf[(size_t)m * K + k] = ld(x, (size_t)m * x_stride + k, act);
+        for (uint32_t k = 0; k < K; ++k) xd[(size_t)m * K + k] = ld(x, (size_t)m * x_stride + k, act);
 #pragma omp parallel
     {
         float* wr = (float*)malloc(sizeof(float) * K);
+        double* wd = (double*)malloc(sizeof(double) * K);
 #pragma omp for schedule(static)
         for (int64_t n = 0; n < (int64_t)N; ++n) {
             deq_row(w, s, wr, (uint32_t)n, K, wfmt, act);
             if (round_dequant && wfmt != LSSM_W_DENSE)
                 for (uint32_t k = 0; k < K; ++k) wr[k] = rnd(wr[k], act);
+            for (uint32_t k = 0; k < K; ++k) wd[k] = wr[k];
+            double dots[4];
             for (uint32_t m = 0; m < M; ++m) {
-                const float* xr = xf + (size_t)m * K;
-                double acc = 0.0;
-                for (uint32_t k = 0; k < K; ++k) acc += (double)wr[k] * (double)xr[k];
-                float a = (float)acc;
+                if (m % 4 == 0 && M - m >= 4) dot4_f64(wd, xd + (size_t)m * K, K, dots);
+                else if (M - (m - m % 4) < 4) dots[m % 4] = dot1_f64(wd, xd + (size_t)m * K, K);
+                float a = (float)dots[m % 4];
                 size_t yi = (size_t)m * y_stride + (size_t)n;
                 if (epi == LSSM_EPI_SILU) a = silu_f(a);
                 if (epi == LSSM_EPI_ADD) a = ld(residual, yi, act) + rnd(a, act);
@@ -282,8 +343,9 @@ void orc_linear(const void* x, uint32_t x_stride, const void* w, const void* s, 
             }
         }
         free(wr);
+        free(wd);
     }
-    free(xf);
+    free(xd);
 }
 
 /* activations.metal:12-21 */
@@ -615,27 +677,44 @@ static void run_block(const orc_model* m, uint32_t li, void* hidden, void* conv_
     void* out = malloc(R * d.d_model * es);
 
     orc_rmsnorm(hidden, bw->norm_w, normed, (uint32_t)R, d.d_model, RMS_EPS, act);
-    /* three in_proj slices (mamba2_block.cpp:150-152): same math as one
-     * projection over all rows; GEMV semantics for decode / L == 1. */
-    int rd = !(decode || L == 1);
-    orc_linear(normed, 0, bw->in_proj_w, bw->in_proj_s, proj, 0, NULL, (uint32_t)R, d.proj,
-               d.d_model, wf, act, LSSM_EPI_NONE, rd);
-    for (size_t r = 0; r < R; ++r) {
-        memcpy((char*)z + r * d.d_inner * es, (char*)proj + r * d.proj * es, d.d_inner * es);
-        memcpy((char*)xbc + r * d.xbc * es, (char*)proj + (r * d.proj + d.d_inner) * es, d.xbc * es);
-        memcpy((char*)dtr + r * d.H * es, (char*)proj + (r * d.proj + d.d_inner + d.xbc) * es, d.H * es);
-    }
     char* cs = (char*)conv_state + (size_t)li * batch * d.xbc * d.K * es;
     float* ss = ssd_state + (size_t)li * batch * d.H * d.P * d.N;
-    /* mamba2_block.cpp:155-170, 183-217: one-row passes (decode, or a 1-token
-     * prefill) use the conv update and the SSD step kernels. */
+    /* mamba2_block.cpp:97-98,130-148: a short prefill (1 < L <= 16) of fp16
+     * weights runs the fused in_proj + conv + SiLU split, whose conv reads the
+     * unrounded fp32 projection (fused.metal:137-149); per sequence, as the
+     * reference's batch-1 model does. */
+    const int fused = !decode && L > 1 && L <= 16 && wf == LSSM_W_DENSE && act == LSSM_F16;
+    int rd = !(decode || L == 1);
     const int step = decode || L == 1;
-    if (step) {
-        orc_conv1d_update(xbc, cs, bw->conv1d_w, bw->conv1d_b, conv, batch, d.xbc, d.K, act);
+    if (fused) {
+        size_t GN = (size_t)d.G * d.N;
+        lssm_fused_inproj_dims fd = {L, d.d_model, d.d_inner, d.N, d.G, d.H, d.K, d.proj};
+        for (uint32_t b = 0; b < batch; ++b) {
+            size_t r0 = (size_t)b * L;
+            orc_inproj_fused((char*)normed + r0 * d.d_model * es, bw->in_proj_w, bw->conv1d_w,
+                             bw->conv1d_b, (char*)z + r0 * d.d_inner * es, (char*)xs + r0 * d.d_inner * es,
+                             (char*)Bs + r0 * GN * es, (char*)Cs + r0 * GN * es, (char*)dtr + r0 * d.H * es,
+                             (char*)xbc + r0 * d.xbc * es, fd, act);
+        }
     } else {
-        orc_conv1d(xbc, bw->conv1d_w, bw->conv1d_b, conv, batch, L, d.xbc, d.K, act);
+        /* three in_proj slices (mamba2_block.cpp:150-152): same math as one
+         * projection over all rows; GEMV semantics for decode / L == 1. */
+        orc_linear(normed, 0, bw->in_proj_w, bw->in_proj_s, proj, 0, NULL, (uint32_t)R, d.proj,
+                   d.d_model, wf, act, LSSM_EPI_NONE, rd);
+        for (size_t r = 0; r < R; ++r) {
+            memcpy((char*)z + r * d.d_inner * es, (char*)proj + r * d.proj * es, d.d_inner * es);
+            memcpy((char*)xbc + r * d.xbc * es, (char*)proj + (r * d.proj + d.d_inner) * es, d.xbc * es);
+            memcpy((char*)dtr + r * d.H * es, (char*)proj + (r * d.proj + d.d_inner + d.xbc) * es, d.H * es);
+        }
+        /* mamba2_block.cpp:155-170, 183-217: one-row passes (decode, or a 1-token
+         * prefill) use the conv update and the SSD step kernels. */
+        if (step) {
+            orc_conv1d_update(xbc, cs, bw->conv1d_w, bw->conv1d_b, conv, batch, d.xbc, d.K, act);
+        } else {
+            orc_conv1d(xbc, bw->conv1d_w, bw->conv1d_b, conv, batch, L, d.xbc, d.K, act);
+        }
+        orc_split_silu_xbc(conv, xs, Bs, Cs, (uint32_t)R, d.d_inner, d.N, d.G, act);
     }
-    orc_split_silu_xbc(conv, xs, Bs, Cs, (uint32_t)R, d.d_inner, d.N, d.G, act);
     if (step) {
         lssm_ssd_step_dims sd = {d.H, d.P, d.N, d.G, DT_MIN, DT_MAX, 1u};
         orc_ssd_step(xs, Bs, Cs, dtr, bw->dt_bias, bw->A_log, bw->D, ss, ys, batch, sd, act);
@@ -656,8 +735,15 @@ static void run_block(const orc_model* m, uint32_t li, void* hidden, void* conv_
     free(xs); free(Bs); free(Cs); free(ys); free(gn); free(out);
 }
 
+/* run_block for one layer on caller-provided hidden rows (the layer-by-layer
+ * parity checks feed it the GPU's hidden state entering layer li). */
+void orc_model_block(const orc_model* m, uint32_t li, void* hidden, void* conv_state, float* ssd_state,
+                     uint32_t batch, uint32_t L, int decode) {
+    run_block(m, li, hidden, conv_state, ssd_state, batch, L, decode);
+}
+
 /* Mamba2Model::compute_logits (mamba2_model.cpp:144-175) for `rows` rows. */
-static void logits_of(const orc_model* m, const void* rows_h, uint32_t rows, void* logits) {
+void orc_model_logits(const orc_model* m, const void* rows_h, uint32_t rows, void* logits) {
     const lssm_model_config* c = &m->cfg;
     int act = (int)c->act;
     size_t es = esz(act);
@@ -682,7 +768,7 @@ void orc_model_prefill(const orc_model* m, void* conv_state, float* ssd_state, c
     for (uint32_t b = 0; b < batch; ++b)
         memcpy((char*)last + (size_t)b * c->d_model * es,
                (char*)hidden + (((size_t)b * L) + L - 1) * c->d_model * es, c->d_model * es);
-    logits_of(m, last, batch, logits);
+    orc_model_logits(m, last, batch, logits);
     free(last);
     free(hidden);
 }
@@ -696,6 +782,6 @@ void orc_model_decode(const orc_model* m, void* conv_state, float* ssd_state, co
     orc_embed(m->embed, ids, hidden, batch, c->d_model, act);
     for (uint32_t li = 0; li < c->n_layer; ++li)
         run_block(m, li, hidden, conv_state, ssd_state, batch, 1, 1);
-    logits_of(m, hidden, batch, logits);
+    orc_model_logits(m, hidden, batch, logits);
     free(hidden);
 }

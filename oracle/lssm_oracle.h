@@ -95,6 +95,14 @@ void orc_model_prefill(const orc_model* m, void* conv_state, float* ssd_state,
                        const int32_t* ids, uint32_t batch, uint32_t L, void* logits);
 void orc_model_decode(const orc_model* m, void* conv_state, float* ssd_state,
                       const int32_t* ids, uint32_t batch, void* logits);
+/* One layer (Mamba2Model::run_block, mamba2_block.cpp:51-290) on caller rows:
+ * hidden [batch * L, d_model] act is updated in place, the layer's slabs of
+ * conv_state / ssd_state ([n_layer, batch, ...]) too.  decode = 1: one token per
+ * sequence (L == 1, conv update + SSD step). */
+void orc_model_block(const orc_model* m, uint32_t li, void* hidden, void* conv_state, float* ssd_state,
+                     uint32_t batch, uint32_t L, int decode);
+/* norm_f + lm_head of `rows` hidden rows (mamba2_model.cpp:144-175) -> logits [rows, vocab]. */
+void orc_model_logits(const orc_model* m, const void* rows_h, uint32_t rows, void* logits);
 
 int orc_num_threads(void);
 void orc_set_num_threads(int n);

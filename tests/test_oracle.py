@@ -161,6 +161,78 @@ def test_rmsnorm_vs_fp64(rng, act):
     assert np.allclose(y, ref, rtol=tol, atol=1e-6)
 
 
+def _round_np(v, act):
+    """fp64 -> activation dtype (RNE) through numpy / torch, not the oracle."""
+    v = np.asarray(v, np.float64)
+    if act == O.F16:
+        return v.astype(np.float16).astype(np.float64)
+    if act == O.BF16:
+        return torch.from_numpy(v.astype(np.float32)).to(torch.bfloat16).to(torch.float64).numpy()
+    return v.astype(np.float32).astype(np.float64)
+
+
+def _ulps(a, b, act):
+    """|a - b| in units of the activation dtype's spacing at |b|."""
+    mant = {O.F16: 10, O.BF16: 7, O.F32: 23}[act]
+    e = np.floor(np.log2(np.maximum(np.abs(b), 2.0 ** -14)))
+    return np.abs(a - b) / 2.0 ** (e - mant)
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_silu_gated_vs_fp64(rng, act):
+    """activations.metal:76-87: y = r(silu(x) * gate), one rounding.  x and gate
+    have different distributions, so silu(gate) * x (swapped operands) or a
+    missing SiLU fails by far more than an ulp."""
+    x = O.to_act(rng.standard_normal(20000) * 3 + 0.5, act)
+    gate = O.to_act(rng.uniform(-2, 2, 20000), act)
+    got = O.from_act(O.silu_gated(x, gate, act), act).astype(np.float64)
+    xf = O.from_act(x, act).astype(np.float64)
+    gf = O.from_act(gate, act).astype(np.float64)
+    ref = _round_np(xf / (1 + np.exp(-xf)) * gf, act)
+    u = _ulps(got, ref, act)
+    # the reference computes silu(x) * gate in fp32 (exp, divide, multiply)
+    # before r(): one ulp at most in fp16 / bf16, a few fp32 ulps in fp32
+    assert u.max() <= (4.0 if act == O.F32 else 1.0), f"max {u.max()} ulp"
+    assert (u == 0).mean() > (0.5 if act == O.F32 else 0.99)
+    swapped = _round_np(gf / (1 + np.exp(-gf)) * xf, act)
+    assert _ulps(got, swapped, act).max() > 100
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_add_inplace_vs_fp64(rng, act):
+    """activations.metal:24-32: y = r(y + x), in place.  Operands of mixed
+    magnitude; the sum of two same-dtype values of nearby exponent is exact in
+    fp32, so the fp64 sum rounded once must match bit for bit."""
+    y0 = O.to_act(rng.standard_normal(20000) * 2, act)
+    x = O.to_act(rng.standard_normal(20000) * 0.5 + 0.25, act)
+    y = y0.copy()
+    O.add_inplace(y, x, act)
+    got = O.from_act(y, act).astype(np.float64)
+    ref = _round_np(O.from_act(y0, act).astype(np.float64) + O.from_act(x, act).astype(np.float64), act)
+    assert np.array_equal(got, ref)
+    # the addend is x, not y again, and nothing is subtracted
+    assert not np.array_equal(got, _round_np(2 * O.from_act(y0, act).astype(np.float64), act))
+
+
+@pytest.mark.parametrize("act", [O.F16, O.BF16])
+def test_gated_rmsnorm_vs_fp64(rng, act):
+    """Gate-then-norm over the full d_inner row (activations.metal:83-86, then
+    norm.metal:52-79): g = r(silu(z) * y), out = r(g * w / sqrt(mean g^2 + eps)),
+    computed here in fp64 with the one intermediate rounding of g."""
+    z = O.to_act(rng.standard_normal((4, 512)), act)
+    y = O.to_act(rng.standard_normal((4, 512)) * 2, act)
+    w = O.to_act(1 + 0.1 * rng.standard_normal(512), act)
+    got = O.from_act(O.gated_rmsnorm(z, y, w, 1e-5, act), act).astype(np.float64)
+    zf, yf, wf = (O.from_act(a, act).astype(np.float64) for a in (z, y, w))
+    g = _round_np(zf / (1 + np.exp(-zf)) * yf, act)
+    ref = _round_np(g * wf / np.sqrt((g ** 2).mean(-1, keepdims=True) + 1e-5), act)
+    assert _ulps(got, ref, act).max() <= 1.0
+    # the gate is silu(z), not silu(y): swapping the roles fails
+    g2 = _round_np(yf / (1 + np.exp(-yf)) * zf, act)
+    ref2 = _round_np(g2 * wf / np.sqrt((g2 ** 2).mean(-1, keepdims=True) + 1e-5), act)
+    assert _ulps(got, ref2, act).max() > 100
+
+
 @pytest.mark.parametrize("act", [O.F16, O.BF16])
 def test_gated_rmsnorm_is_gate_then_norm(rng, act):
     z = O.to_act(rng.standard_normal((4, 512)), act)
@@ -415,6 +487,30 @@ def test_model_prefill_plus_step_equals_longer_prefill(rng):
     assert np.allclose(lg_step, lg_full, rtol=1e-4, atol=1e-4)
     assert np.allclose(s1, s2, rtol=1e-4, atol=1e-5)
     assert np.allclose(c1, c2, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("L", [2, 12, 16, 17])
+def test_model_short_fp16_prefill_vs_token_steps(rng, L):
+    """fp16 dense weights: a prefill of 1 < L <= 16 tokens takes the reference's
+    fused in_proj + conv branch (mamba2_block.cpp:97-98,130-148; the conv reads
+    the unrounded projection), longer ones the chunked path.  Either way it
+    must agree, within fp16 rounding, with L single-token steps from a zero
+    state (the decode recurrence), in logits, SSD state and conv state.  (The
+    fused op itself equals the unfused chain up to that rounding:
+    test_inproj_fused_vs_unfused_chain.)"""
+    m = _tiny_host_model(rng, O.F16, O.W_DENSE, G=2)
+    ids = rng.integers(0, 97, (2, L)).astype(np.int32)
+    c1, s1 = m.new_state(2)
+    lg = O.from_act(m.prefill(c1, s1, ids), O.F16)
+    c2, s2 = m.new_state(2)
+    for t in range(L):
+        lg_s = O.from_act(m.decode(c2, s2, np.ascontiguousarray(ids[:, t])), O.F16)
+    assert np.abs(lg - lg_s).max() <= 2e-2 * np.abs(lg_s).max()
+    assert np.abs(s1 - s2).max() <= 2e-2 * np.abs(s2).max()
+    # the conv window holds the last K pre-conv projections: rounded once on
+    # both routes, from projections that differ only by rounding
+    cf, cs = O.from_act(c1, O.F16), O.from_act(c2, O.F16)
+    assert np.abs(cf - cs).max() <= 2e-2 * np.abs(cs).max()
 
 
 @pytest.mark.parametrize("act,wfmt", [(O.F16, O.W_Q4_B32), (O.BF16, O.W_Q4_G64), (O.F16, O.W_Q8_G32)])
