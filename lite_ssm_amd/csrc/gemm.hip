@@ -226,8 +226,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs a) {
 // reference GEMM does) into a 2-stage ring one step ahead; dense W goes by
 // DMA into a 3-stage ring.  So loads and dequantization run beside the
 // MFMAs instead of between them.  One barrier per K step.  LDS rows are 64
-// elements (128 B) whose 16-byte slots are XOR-swizzled by row % 8, so the
-// fragment reads of 8 consecutive rows hit distinct banks without padding.
+// elements (128 B) whose 16-byte slots are XOR-swizzled by swz(row), so the
+// fragment reads of 16 consecutive rows hit distinct banks without padding.
 // ---------------------------------------------------------------------------
 constexpr int G2M = 256, G2K = 64;
 
@@ -306,6 +306,13 @@ template <typename T> __device__ __forceinline__ uint32_t lds_addr(const T* p) {
     return (uint32_t)(size_t)((const __attribute__((address_space(3))) T*)p);
 }
 
+// LDS tile rows are 128 B (64 16-bit elements, 8 slots of 16 B) and the
+// banks repeat every 256 B, so rows r and r + 2 share banks.  Physical slot =
+// logical slot ^ ((r / 2) % 8): 16 consecutive rows read or written at one
+// logical slot then cover all 16 16-byte positions of the 256 B window (row
+// parity picks the half, the XOR the position), with no bank conflict.
+__device__ __forceinline__ constexpr uint32_t swz(uint32_t row) { return (row >> 1) & 7u; }
+
 // Workgroups go to the 8 XCDs round-robin in launch order (linear id % 8),
 // and each XCD has its own L2.  Give XCD x a contiguous run of the tiles in
 // M-major order, so the blocks that share an X row block (all N tiles of one
@@ -355,12 +362,12 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
         const uint32_t p = t - 64 * CW;
         if constexpr (DENSE) {
             // by DMA: producer wave q fills tile rows 32 q .. + 32, 8 rows per
-            // instruction (lane i: row + i / 8, physical slot i % 8 = logical
-            // slot (i % 8) ^ (i / 8)); rows past N re-read row N - 1.
-            const uint32_t sl = (lane % 8) ^ (lane / 8);
+            // instruction (lane i: row r = run + i / 8, physical slot i % 8 =
+            // logical slot (i % 8) ^ swz(r)); rows past N re-read row N - 1.
             const char* wq[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                const uint32_t sl = (lane % 8) ^ swz(8 * j + lane / 8);
                 const uint32_t n = min(n0 + 32 * q + 8 * j + lane / 8, a.N - 1);
                 wq[j] = (const char*)a.w + ((size_t)n * K + 8 * sl) * sizeof(T);
             }
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
             };
             auto store_w = [&](uint32_t kt, const R (&r)[CPT]) {
                 T* Brow = Bs[kt % SB] + br * G2K;
-                const uint32_t sw = br % 8;
+                const uint32_t sw = swz(br);
 #pragma unroll
                 for (int h = 0; h < CPT; ++h) {
                     uint32_t d[8];
@@ -442,14 +449,15 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
 
     // ---------------- compute waves: 128 x 64 of Y each ----------------
     // They also DMA X: wave c fills tile rows XR c .. + XR of the stage two
-    // steps ahead, 8 rows per instruction (lane i: row + i / 8, physical slot
-    // i % 8 = logical slot (i % 8) ^ (i / 8)); rows past M re-read row M - 1.
+    // steps ahead, 8 rows per instruction (lane i: row r = run + i / 8,
+    // physical slot i % 8 = logical slot (i % 8) ^ swz(r); XR c is a multiple
+    // of 16); rows past M re-read row M - 1.
     const int wm = w / (CW / 2), wn = w % (CW / 2);
-    const uint32_t xl = (lane % 8) ^ (lane / 8);
     constexpr int XJ = XR / 8;                    // DMA instructions per step
     uint32_t xo[XJ];
 #pragma unroll
     for (int j = 0; j < XJ; ++j) {
+        const uint32_t xl = (lane % 8) ^ swz(8 * j + lane / 8);
         const uint32_t m = min(m0 + XR * w + 8 * j + lane / 8, a.M - 1);
         xo[j] = (m * a.x_stride + 8 * xl) * (uint32_t)sizeof(T);
     }
@@ -467,10 +475,11 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    // fragment offsets (elements): row & 7 == lane & 7 for every fragment
+    // fragment offsets (elements): fragment rows are 32 i + lane % 32 (tile
+    // bases are multiples of 16), so swz(row) == swz(lane % 32)
     uint32_t fo[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) fo[ks] = (lane % 32) * G2K + 8 * ((2 * ks + lane / 32) ^ (lane % 8));
+    for (int ks = 0; ks < 4; ++ks) fo[ks] = (lane % 32) * G2K + 8 * ((2 * ks + lane / 32) ^ swz(lane % 32));
 
     // XJ DMAs per step: vmcnt(XJ) = the previous step's are done
     auto wait_prev = [] {

@@ -168,9 +168,16 @@ struct SsdArgs {
     int act;
     // optional gate (decode engine): Y = r(silu(z) * r(y)); z row stride
     const void* z;  uint32_t z_stride;
+    // chunked scan, optional: scratch of ssd_gram_floats(batch, L, G) floats for
+    // the chunks' C B^T Gram tiles, computed once per (sequence, chunk, group)
+    // and shared by the group's heads (null: every head computes its own)
+    float* gram = nullptr;
 };
 hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a);
 hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a);
+inline size_t ssd_gram_floats(uint32_t batch, uint32_t L, uint32_t G) {
+    return (size_t)batch * ((L + 63) / 64) * G * 64 * 64;
+}
 
 hipError_t launch_inproj_fused(hipStream_t s, const void* normed, const void* W_in,
                                const void* W_conv, const void* conv_b, void* proj_z, void* ssd_x,

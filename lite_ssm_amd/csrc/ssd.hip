@@ -10,6 +10,7 @@
 // with S held in the activation dtype between chunks (the reference keeps it
 // in `half` threadgroup memory) and written back as fp32.
 #include <cfloat>
+#include <cstdlib>
 
 #include "common.cuh"
 #include "internal.hpp"
@@ -290,10 +291,56 @@ template <typename T> __device__ __forceinline__ floatx4 unpack4(s4v v) {
     return r;
 }
 
-template <typename T, int NW>
-__global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
-    constexpr int NT = 64 * NW;           // threads
+// The chunks' Gram tiles G[t][j] = C_t . B_j (fp32, t, j < 64), which depend
+// only on the sequence, the chunk and the group: computed once here and read
+// by every head of the group (and P slice) in ssd_chunk_mfma_kernel instead of
+// being recomputed there.  Block (chunk, group, sequence), four waves; the ten
+// tiles with J <= T (16-token blocks) only, on the same MFMA with the same
+// operands as the in-kernel computation, so the values are identical.  The
+// operands are read straight from global memory: both have k = n contiguous.
+// Tokens past the end of the last chunk re-read token t0 (their entries are
+// masked by the scan).
+template <typename T>
+__global__ __launch_bounds__(256) void ssd_gram_kernel(SsdArgs a) {
+    const uint32_t c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const uint32_t L = a.L, nch = (L + CQ - 1) / CQ, t0 = c * CQ;
+    const uint32_t tl = min((uint32_t)CQ, L - t0);
+    const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
+    const int li = lane % 16, lq = lane / 16;
+    const T* Bv = (const T*)a.B + ((size_t)b * L + t0) * a.b_stride + (size_t)g * CN;
+    const T* Cv = (const T*)a.C + ((size_t)b * L + t0) * a.c_stride + (size_t)g * CN;
+    float* out = a.gram + (((size_t)b * nch + c) * a.G + g) * (CQ * CQ);
+    // (J, T) of the ten lower tiles, 2 + 2 bits each
+    constexpr uint64_t JT = 0x0ull | 0x4ull << 4 | 0x5ull << 8 | 0x8ull << 12 | 0x9ull << 16 | 0xAull << 20 |
+                            0xCull << 24 | 0xDull << 28 | 0xEull << 32 | 0xFull << 36;
+    for (int kt = w; kt < 10; kt += 4) {
+        const int jt = (int)(JT >> (4 * kt)) & 15;
+        const int J = jt & 3, Tt = jt >> 2;
+        const uint32_t j = 16 * J + li, t = 16 * Tt + li;
+        const T* br = Bv + (size_t)(j < tl ? j : 0) * a.b_stride + 8 * lq;
+        const T* cr = Cv + (size_t)(t < tl ? t : 0) * a.c_stride + 8 * lq;
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < CN / 32; ++ks)
+            acc = mma16<T>(*reinterpret_cast<const s8v*>(br + 32 * ks), *reinterpret_cast<const s8v*>(cr + 32 * ks), acc);
+        // acc[r] = B_{16J + 4lq + r} . C_t  ->  G[t][16J + 4lq .. + 3]
+        *reinterpret_cast<floatx4*>(out + (size_t)t * CQ + 16 * J + 4 * lq) = acc;
+    }
+}
+
+// SPL = 2: two waves per 16-column slice.  Wave (slice cs, half hh) computes
+// the output token tiles 2 hh, 2 hh + 1 and updates state tiles n = 64 hh ..
+// + 63 (it keeps the whole state of its columns, the k = n operand of C . S);
+// the halves trade their updated state tiles through LDS at the mid-chunk
+// barrier.  The serial chain per chunk is then about half as long, and a CU
+// holds twice the waves.
+template <typename T, int NW, bool GP, int SPL>
+__global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a) {
+    constexpr int NWV = NW * SPL;         // waves
+    constexpr int NT = 64 * NWV;          // threads
     constexpr int PB = 16 * NW;           // state columns p per block
+    constexpr int NTT = 4 / SPL;          // output token tiles per wave
+    constexpr int NST = 8 / SPL;          // state n-tiles a wave updates
     constexpr int XP = PB + 8;            // X row pitch
     constexpr int BV = CQ * CN / 8 / NT;  // 16-byte pieces of B (and of C) per thread
     constexpr int XV = CQ * PB / 8 / NT;  // 16-byte pieces of X per thread (= 2)
@@ -306,6 +353,8 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
     // per-token chunk scalars, double-buffered: wave 0 computes chunk c + 1's
     // while the block works on chunk c
     __shared__ __attribute__((aligned(16))) float LCb[2][CQ], DTb[2][CQ], ELb[2][CQ], Wb[2][CQ];
+    // SPL = 2: each wave's updated state tiles for its partner
+    __shared__ __attribute__((aligned(16))) s4v Sx[SPL == 2 ? NWV * NST * 64 : 1];
 
     const uint32_t P = a.P, H = a.H, L = a.L;
     const uint32_t npb = P / PB;
@@ -328,7 +377,8 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(tid / WAVE);
     const int li = lane % 16, lq = lane / 16;
     const int tk = li / 4, tc = li % 4;    // transpose-load row block / column piece
-    const int pw = 16 * w;                 // this wave's columns within the block
+    const int cs = w % NW, hh = SPL == 1 ? 0 : w / NW;   // column slice, half (SPL = 2)
+    const int pw = 16 * cs;                // this wave's columns within the block
 
     // S^T tiles, rounded to T and packed: sp[nt][r] = S[p = pw + li][n = 16 nt + 4 lq + r]
     s4v sp[8];
@@ -355,8 +405,27 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
     u32x4 rb[BV], rc[BV], rx[XV];   // (vector types: a struct uint4 copies
                                     // through memory and stays in scratch)
     uint32_t rdt = 0;
+    // Gram tiles of this wave's M positions (GP): next chunk's in flight,
+    // current chunk's in use
+    constexpr int NTL = (12 + NWV - 1) / NWV;
+    constexpr uint64_t JT = 0x1ull | 0x0ull << 4 | 0x4ull << 8 | 0x5ull << 12 | 0xBull << 16 |
+                            0x8ull << 20 | 0x9ull << 24 | 0xAull << 28 | 0xCull << 32 |
+                            0xDull << 36 | 0xEull << 40 | 0xFull << 44;
+    floatx4 rgn[GP ? NTL : 1], rgc[GP ? NTL : 1];
+    const uint32_t nchk = (L + CQ - 1) / CQ;
     auto fetch = [&](uint32_t t0) {
         const uint32_t tl = min((uint32_t)CQ, L - t0);
+        if constexpr (GP) {
+            const float* gc = a.gram + (((size_t)b * nchk + t0 / CQ) * a.G + g) * (CQ * CQ);
+#pragma unroll
+            for (int i = 0; i < NTL; ++i) {
+                const int kt = w + NWV * i;
+                const int jt = (int)(JT >> (4 * kt)) & 15;
+                const int J = jt & 3, Tt = jt >> 2;
+                if (kt < 12 && kt != 0 && kt != 4)
+                    rgn[i] = *reinterpret_cast<const floatx4*>(gc + (size_t)(16 * Tt + li) * CQ + 16 * J + 4 * lq);
+            }
+        }
         if (tl == CQ) {
 #pragma unroll
             for (int v = 0; v < BV; ++v) {
@@ -382,6 +451,10 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
         if (w == 0) rdt = raw_of(dtr + (size_t)(t0 + min((uint32_t)lane, tl - 1)) * a.dt_stride);
     };
     auto stage = [&]() {
+        if constexpr (GP) {
+#pragma unroll
+            for (int i = 0; i < NTL; ++i) rgc[i] = rgn[i];
+        }
 #pragma unroll
         for (int v = 0; v < BV; ++v) {
             *reinterpret_cast<u32x4*>(Bs + (brow + BR * v) * SPAD + bcol) = rb[v];
@@ -434,25 +507,26 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
         // an immediate (an indexed array would be a memory load whose wait
         // would also wait for the prefetch). ----
         {
-            constexpr int NTL = 12 / NW;
-            constexpr uint64_t JT = 0x1ull | 0x0ull << 4 | 0x4ull << 8 | 0x5ull << 12 | 0xBull << 16 |
-                                    0x8ull << 20 | 0x9ull << 24 | 0xAull << 28 | 0xCull << 32 |
-                                    0xDull << 36 | 0xEull << 40 | 0xFull << 44;
             const float* DTs = DTb[c & 1];
 #pragma unroll
             for (int i = 0; i < NTL; ++i) {
-                const int kt = w + NW * i;
+                const int kt = w + NWV * i;
+                if (kt >= 12) break;
                 const int jt = (int)(JT >> (4 * kt)) & 15;
                 const int J = jt & 3, Tt = jt >> 2;
                 const int t = 16 * Tt + li;
                 s4v m4 = {0, 0, 0, 0};
                 if (kt != 0 && kt != 4) {
                     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if constexpr (GP) {
+                        acc = rgc[i];
+                    } else {
 #pragma unroll
-                    for (int ks = 0; ks < CN / 32; ++ks) {
-                        const s8v af = *reinterpret_cast<const s8v*>(Bs + (16 * J + li) * SPAD + 32 * ks + 8 * lq);
-                        const s8v bf = *reinterpret_cast<const s8v*>(Cs + t * SPAD + 32 * ks + 8 * lq);
-                        acc = mma16<T>(af, bf, acc);
+                        for (int ks = 0; ks < CN / 32; ++ks) {
+                            const s8v af = *reinterpret_cast<const s8v*>(Bs + (16 * J + li) * SPAD + 32 * ks + 8 * lq);
+                            const s8v bf = *reinterpret_cast<const s8v*>(Cs + t * SPAD + 32 * ks + 8 * lq);
+                            acc = mma16<T>(af, bf, acc);
+                        }
                     }
                     const float lct = LCs[t];
                     const floatx4 lcj = *reinterpret_cast<const floatx4*>(LCs + 16 * J + 4 * lq);
@@ -484,9 +558,12 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
 
         // ---- e^{Lcum_t} (S_p . C_t) for the 4 token tiles; S is the
         // k = n operand as it lies in registers ----
+        // (register arrays are indexed by unrolled constants only: the wave's
+        // half hh selects tiles by a wave-uniform branch)
         floatx4 yacc[4];
 #pragma unroll
         for (int Tt = 0; Tt < 4; ++Tt) {
+            if (Tt / NTT != hh) continue;
             const int t = 16 * Tt + li;
             floatx4 yo = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -516,6 +593,7 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
             }
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
+                if (nt / NST != hh) continue;
                 floatx4 acc = unpack4<T>(sp[nt]);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[r] *= dch;
@@ -526,9 +604,16 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
                     acc = mma16<T>(bt, wx[ka], acc);
                 }
                 sp[nt] = pack4<T>(acc);
+                if constexpr (SPL == 2) Sx[(w * NST + nt % NST) * 64 + lane] = sp[nt];
             }
         }
-        __syncthreads();   // M complete; staging no longer read
+        __syncthreads();   // M complete; staging no longer read; state halves posted
+        if constexpr (SPL == 2) {
+            const int pw2 = (w + NW) % NWV;                 // the partner wave
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt)
+                if (nt / NST != hh) sp[nt] = Sx[(pw2 * NST + nt % NST) * 64 + lane];
+        }
 
         // Stage the next chunk first: its loads were issued a chunk ago, and
         // waiting for them before the Y stores below keeps those stores out
@@ -538,6 +623,7 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
         // ---- Y^T += X^T M^T + X^T (D I), store ----
 #pragma unroll
         for (int Tt = 0; Tt < 4; ++Tt) {
+            if (Tt / NTT != hh) continue;
             const int t = 16 * Tt + li;
 #pragma unroll
             for (int ka = 0; ka < 2; ++ka) {
@@ -554,7 +640,173 @@ __global__ __launch_bounds__(64 * NW) void ssd_chunk_mfma_kernel(SsdArgs a) {
     }
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
-        *reinterpret_cast<floatx4*>(st + (size_t)(pw + li) * CN + 16 * nt + 4 * lq) = unpack4<T>(sp[nt]);
+        if (nt / NST == hh)
+            *reinterpret_cast<floatx4*>(st + (size_t)(pw + li) * CN + 16 * nt + 4 * lq) = unpack4<T>(sp[nt]);
+}
+
+
+// ---------------------------------------------------------------------------
+// Chunked scan for fp32 activations on v_mfma_f32_16x16x4_f32 (chunk 64,
+// N = 128, P % 64 == 0).  No rounding between the steps (the activation dtype
+// is fp32), so this is ssd_chunked.metal's arithmetic in fp32 throughout.
+// Block (h * P / 64 + pb, b), four waves, wave w owns state columns
+// p = 16 w .. + 16.  Per chunk, B, C and X are staged in LDS, wave 0 scans DT
+// and Lcum, the waves split the ten lower tiles of G = C B^T into
+// M[t][j] = G e^{Lc_t - Lc_j} DT_j (LDS), then each wave computes
+//   Y^T[p][t] = e^{Lc_t} (S C^T)[p][t] + (X^T M^T)[p][t] + D x[t][p]
+//   S^T[n][p] = e^{L_end} S^T[n][p] + (B^T (w o X))[n][p]
+// with its state tiles S^T in registers, laid out exactly as the S update's
+// MFMA writes them.  16x16x4 operands: lane l supplies A[l % 16][k = l / 16]
+// and B[k = l / 16][l % 16]; D[4 (l / 16) + r][l % 16] comes back in element
+// r.  The k order inside a product is free as long as both operands follow
+// it, so it is chosen per product to keep the LDS reads conflict-free: state
+// row i = 4 q + r of tile nt is n = 64 (nt / 4) + 16 q + 4 (nt % 4) + r.  LDS
+// pitches (floats): C 129 (= 1 mod 64 banks), B 132 (= 4), X 80 (= 16),
+// M 68 (= 4).
+// ---------------------------------------------------------------------------
+constexpr int F_CP = 129, F_BP = 132, F_XP = 80, F_MP = 68;
+
+__device__ __forceinline__ int f_srow(int nt, int i) {   // state row (n) of tile nt, row i
+    return 64 * (nt / 4) + 16 * (i / 4) + 4 * (nt % 4) + (i % 4);
+}
+__device__ __forceinline__ floatx4 mma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
+    __shared__ float Cs[CQ * F_CP];
+    __shared__ float Bs[CQ * F_BP];
+    __shared__ float Xs[CQ * F_XP];
+    __shared__ float Ms[CQ * F_MP];
+    __shared__ float LCs[CQ], DTs[CQ], ELs[CQ], Ws[CQ];
+
+    const uint32_t P = a.P, H = a.H, L = a.L;
+    const uint32_t npb = P / 64;
+    const uint32_t h = blockIdx.x / npb, pb = blockIdx.x % npb, b = blockIdx.y;
+    const uint32_t p0 = pb * 64;
+    const uint32_t hpg = (H / a.G) > 0 ? H / a.G : 1;
+    const uint32_t g = h / hpg;
+    const float* X = (const float*)a.X + (size_t)b * L * a.x_stride + (size_t)h * P + p0;
+    const float* Bv = (const float*)a.B + (size_t)b * L * a.b_stride + (size_t)g * CN;
+    const float* Cv = (const float*)a.C + (size_t)b * L * a.c_stride + (size_t)g * CN;
+    const float* dtr = (const float*)a.dt + (size_t)b * L * a.dt_stride + h;
+    float* Y = (float*)a.Y + (size_t)b * L * a.y_stride + (size_t)h * P + p0;
+    float* st = a.state + (((size_t)b * H + h) * P + p0) * CN;
+    const float A_h = -expf(((const float*)a.A_log)[h]);
+    const float dt_b = ((const float*)a.dt_bias)[h];
+    const float D_h = a.has_D ? ((const float*)a.D)[h] : 0.0f;
+
+    const int tid = threadIdx.x, lane = tid % WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int li = lane % 16, lq = lane / 16;
+    const int pw = 16 * w;
+
+    // S^T tiles: sT[nt][r] = S[p = pw + li][n = f_srow(nt, 4 lq + r)] (4 consecutive n)
+    floatx4 sT[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+        sT[nt] = *reinterpret_cast<const floatx4*>(st + (size_t)(pw + li) * CN + f_srow(nt, 4 * lq));
+
+    const uint32_t nch = (L + CQ - 1) / CQ;
+    for (uint32_t c = 0; c < nch; ++c) {
+        const uint32_t t0 = c * CQ, tl = min((uint32_t)CQ, L - t0);
+        // ---- stage the chunk (rows past tl as zeros) and scan DT / Lcum ----
+        for (uint32_t i = tid; i < CQ * CN; i += 256) {
+            const uint32_t t = i / CN, n = i % CN;
+            Cs[t * F_CP + n] = t < tl ? Cv[(size_t)(t0 + t) * a.c_stride + n] : 0.0f;
+            Bs[t * F_BP + n] = t < tl ? Bv[(size_t)(t0 + t) * a.b_stride + n] : 0.0f;
+        }
+        for (uint32_t i = tid; i < CQ * 64; i += 256) {
+            const uint32_t t = i / 64, pp = i % 64;
+            Xs[t * F_XP + pp] = t < tl ? X[(size_t)(t0 + t) * a.x_stride + pp] : 0.0f;
+        }
+        if (w == 0) {
+            float dv = 0.0f;
+            if ((uint32_t)lane < tl) {
+                dv = softplus_f(dtr[(size_t)(t0 + lane) * a.dt_stride] + dt_b);
+                dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
+            }
+            float v = A_h * dv;
+#pragma unroll
+            for (int off = 1; off < WAVE; off <<= 1) {
+                const float o = __shfl_up(v, off, WAVE);
+                if (lane >= off) v += o;
+            }
+            const float l_end = __shfl(v, WAVE - 1, WAVE);
+            LCs[lane] = v;
+            DTs[lane] = dv;
+            ELs[lane] = expf(v);
+            Ws[lane] = expf(l_end - v) * dv;
+        }
+        __syncthreads();
+        // ---- M = G e^{Lc_t - Lc_j} DT_j on the ten lower tiles (J <= T) ----
+        for (int kt = w; kt < 10; kt += 4) {
+            constexpr uint64_t JT = 0x0ull | 0x4ull << 4 | 0x5ull << 8 | 0x8ull << 12 | 0x9ull << 16 |
+                                    0xAull << 20 | 0xCull << 24 | 0xDull << 28 | 0xEull << 32 | 0xFull << 36;
+            const int jt = (int)(JT >> (4 * kt)) & 15;
+            const int J = jt & 3, Tt = jt >> 2;
+            floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            // A = C rows t, B = B^T columns j; k = n = 16 q + ks % 16 + 64 (ks / 16)
+            const float* cr = Cs + (16 * Tt + li) * F_CP + 16 * lq;
+            const float* br = Bs + (16 * J + li) * F_BP + 16 * lq;
+#pragma unroll
+            for (int ks = 0; ks < 32; ++ks) {
+                const int n = (ks % 16) + 64 * (ks / 16);
+                acc = mma4(cr[n], br[n], acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * Tt + 4 * lq + r, j = 16 * J + li;
+                const float mv = acc[r] * expf(fminf(LCs[t] - LCs[j], 0.0f)) * DTs[j];
+                Ms[t * F_MP + j] = (j <= t && (uint32_t)t < tl) ? mv : 0.0f;
+            }
+        }
+        __syncthreads();   // (token tile Tt reads M columns j < 16 (Tt + 1) only)
+        // ---- Y^T for this wave's columns ----
+#pragma unroll
+        for (int Tt = 0; Tt < 4; ++Tt) {
+            floatx4 yo = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float* cr = Cs + (16 * Tt + li) * F_CP;
+#pragma unroll
+            for (int ks = 0; ks < 32; ++ks) {
+                const int nt = ks / 4, r = ks % 4;
+                yo = mma4(sT[nt][r], cr[f_srow(nt, 4 * lq + r)], yo);
+            }
+            const float el = ELs[16 * Tt + li];
+            floatx4 y;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[r] = yo[r] * el;
+            // + X^T M^T over j <= 16 Tt + 15
+            for (int kk = 0; kk < 4 * (Tt + 1); ++kk)
+                y = mma4(Xs[(4 * kk + lq) * F_XP + pw + li], Ms[(16 * Tt + li) * F_MP + 4 * kk + lq], y);
+            const int t = 16 * Tt + li;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[r] += D_h * Xs[t * F_XP + pw + 4 * lq + r];
+            if ((uint32_t)t < tl)
+                *reinterpret_cast<floatx4*>(Y + (size_t)(t0 + t) * a.y_stride + pw + 4 * lq) = y;
+        }
+        // ---- S^T = e^{L_end} S^T + B^T (w o X) ----
+        {
+            const float dch = expf(LCs[CQ - 1]);
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) {
+                floatx4 acc = sT[nt];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] *= dch;
+                const int n = f_srow(nt, li);
+#pragma unroll
+                for (int kk = 0; kk < 16; ++kk) {
+                    const int j = 4 * kk + lq;
+                    acc = mma4(Bs[j * F_BP + n], Ws[j] * Xs[j * F_XP + pw + li], acc);
+                }
+                sT[nt] = acc;
+            }
+        }
+        __syncthreads();   // staging and M no longer read
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+        *reinterpret_cast<floatx4*>(st + (size_t)(pw + li) * CN + f_srow(nt, 4 * lq)) = sT[nt];
 }
 
 template <typename T, bool GATE>
@@ -596,15 +848,46 @@ hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a) {
         // Four waves (64 columns of P) per block when that still gives a
         // block per CU; otherwise two, for more blocks.
         const bool nw4 = (a.P % 64) == 0 && (size_t)a.batch * a.H * (a.P / 64) >= (size_t)num_cus();
-        if (nw4) {
-            const dim3 grid(a.H * (a.P / 64), a.batch);
-            if (a.act == LSSM_F16) ssd_chunk_mfma_kernel<f16, 4><<<grid, 256, 0, s>>>(a);
-            else ssd_chunk_mfma_kernel<bf16, 4><<<grid, 256, 0, s>>>(a);
-        } else {
-            const dim3 grid(a.H * (a.P / 32), a.batch);
-            if (a.act == LSSM_F16) ssd_chunk_mfma_kernel<f16, 2><<<grid, 128, 0, s>>>(a);
-            else ssd_chunk_mfma_kernel<bf16, 2><<<grid, 128, 0, s>>>(a);
-        }
+        const bool gp = a.gram != nullptr;
+        auto go = [&](auto tag) {
+            using T = decltype(tag);
+            if (gp) {
+                const dim3 gg((a.L + CQ - 1) / CQ, a.G, a.batch);
+                ssd_gram_kernel<T><<<gg, 256, 0, s>>>(a);
+            }
+            // two waves per 16-column slice (SPL = 2) when the grid does not
+            // fill the chip anyway (then every block has a CU to itself and
+            // the shorter chain wins; with more blocks than CUs the larger
+            // register footprint of SPL = 2 costs a second round of blocks)
+            const size_t nblk = (size_t)a.batch * a.H * (a.P / (nw4 ? 64 : 32));
+            const bool split = nblk <= (size_t)num_cus();
+            if (nw4) {
+                const dim3 grid(a.H * (a.P / 64), a.batch);
+                if (split) {
+                    if (gp) ssd_chunk_mfma_kernel<T, 4, true, 2><<<grid, 512, 0, s>>>(a);
+                    else ssd_chunk_mfma_kernel<T, 4, false, 2><<<grid, 512, 0, s>>>(a);
+                } else {
+                    if (gp) ssd_chunk_mfma_kernel<T, 4, true, 1><<<grid, 256, 0, s>>>(a);
+                    else ssd_chunk_mfma_kernel<T, 4, false, 1><<<grid, 256, 0, s>>>(a);
+                }
+            } else {
+                const dim3 grid(a.H * (a.P / 32), a.batch);
+                if (split) {
+                    if (gp) ssd_chunk_mfma_kernel<T, 2, true, 2><<<grid, 256, 0, s>>>(a);
+                    else ssd_chunk_mfma_kernel<T, 2, false, 2><<<grid, 256, 0, s>>>(a);
+                } else {
+                    if (gp) ssd_chunk_mfma_kernel<T, 2, true, 1><<<grid, 128, 0, s>>>(a);
+                    else ssd_chunk_mfma_kernel<T, 2, false, 1><<<grid, 128, 0, s>>>(a);
+                }
+            }
+        };
+        if (a.act == LSSM_F16) go(f16{});
+        else go(bf16{});
+        return hipGetLastError();
+    }
+    if (a.act == LSSM_F32 && chunk_ok && a.N == CN && (a.P % 64) == 0 && ((uintptr_t)a.state % 16 == 0) &&
+        ((uintptr_t)a.Y % 16 == 0) && (a.y_stride % 4 == 0)) {
+        ssd_chunk_f32_mfma_kernel<<<dim3(a.H * (a.P / 64), a.batch), 256, 0, s>>>(a);
         return hipGetLastError();
     }
     if (a.chunk > (uint32_t)SC_MAXCK || a.N > (uint32_t)SC_MAXN) return hipErrorInvalidValue;

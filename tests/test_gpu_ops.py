@@ -338,6 +338,26 @@ def test_ssd_chunked_config1_fp32(ctx, rng):
     assert max_rel(host(sd, np.float32), s2) < 1e-3
 
 
+@pytest.mark.parametrize("batch,Lq,H,G,P", [(1, 512, 24, 1, 64), (2, 200, 8, 2, 128), (1, 40, 4, 1, 64),
+                                            (3, 64, 16, 8, 64)])
+def test_ssd_chunked_fp32_mfma_vs_oracle(ctx, rng, batch, Lq, H, G, P):
+    """The fp32 chunked scan on v_mfma_f32_16x16x4_f32: a nonzero initial
+    state, ragged last chunks, several groups and P slices, max-rel 1e-3 on y
+    and the final state."""
+    L = _lib()
+    act, N = O.F32, 128
+    X, B, Cc, dt, dtb, A_log, D = _ssd_inputs(rng, batch, Lq, H, P, N, G, act)
+    s0 = (rng.standard_normal((batch, H, P, N)) * 0.3).astype(np.float32)
+    sd = dev(s0)
+    Y = empty((batch, Lq, H, P), act)
+    ctx.ssd_chunked(dev(X), dev(B), dev(Cc), dev(dt), dev(dtb), dev(A_log), dev(D), Y, sd, batch,
+                    L.SSDDims(Lq, H, P, N, G, 64, 1e-6, 1e6, 1), act)
+    s2 = s0.copy()
+    Yr = O.ssd_chunked(X, B, Cc, dt, dtb, A_log, D, s2, batch, Lq, H, P, N, G, 64, act)
+    assert max_rel(host(Y, np.float32), Yr) < 1e-3
+    assert max_rel(host(sd, np.float32), s2) < 1e-3
+
+
 # (4, 130, 64, 1) and P = 128 give at least one block per CU with four waves
 # per block (64 state columns); the others take the two-wave blocks.
 @pytest.mark.parametrize("act", [O.F16, O.BF16])
