@@ -318,6 +318,24 @@ int lssm_inproj_ssd_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w
                            uint32_t n_groups, uint32_t n_heads, uint32_t d_head, uint32_t d_conv,
                            float eps, lssm_wfmt wfmt, lssm_dtype act);
 
+/* lssm_inproj_ssd_decode that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops).  The projection's tagged words
+ * and the step tag live in a static device array of the library (512 KiB +
+ * 256 B, held by each GPU the library runs on until the process ends; zero at
+ * load), and the tag is advanced on the device before each launch, so the
+ * caller keeps no tag.  Shapes whose d_inner + xBC_dim + n_heads
+ * exceeds 65536 projection rows are refused (LSSM_EINVAL), as are those the
+ * fused launch does not take.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, two threads) race on it. */
+int lssm_inproj_ssd_decode_noalloc(lssm_ctx* ctx, const void* hidden, const void* norm_w, const void* w,
+                                   const void* w_scales, void* conv_state, const void* conv_w,
+                                   const void* conv_b, const void* dt_bias, const void* A_log,
+                                   const void* D_skip, float* ssd_state, void* y, uint32_t d_model,
+                                   uint32_t d_inner, uint32_t d_state, uint32_t n_groups, uint32_t n_heads,
+                                   uint32_t d_head, uint32_t d_conv, float eps, lssm_wfmt wfmt,
+                                   lssm_dtype act);
+
 /* Batch-1 decode of one layer's whole mixer in ONE launch (in place on
  * `hidden` [d_model]): lssm_inproj_ssd_decode, then r(gated RMSNorm(y)) (the
  * mixer norm, norm.metal:52-79), out_proj and the residual add, hidden =

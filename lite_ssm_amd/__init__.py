@@ -160,6 +160,7 @@ _SIGS = {
     "lssm_ssd_step": ([_vp] + [_vp] * 9 + [_u32, SSDStepDims, _i], _i),
     "lssm_inproj_decode": ([_vp] * 11 + [_u32] * 7 + [_f, _i, _i], _i),
     "lssm_inproj_ssd_decode": ([_vp] * 14 + [_u32] * 8 + [_f, _i, _i], _i),
+    "lssm_inproj_ssd_decode_noalloc": ([_vp] * 13 + [_u32] * 7 + [_f, _i, _i], _i),
     "lssm_mixer_decode": ([_vp] * 16 + [_u32] * 8 + [_f, _i, _i], _i),
     "lssm_embed": ([_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i], _i),
     "lssm_argmax": ([_vp, _vp, _vp, _u32, _u32, _i], _i),

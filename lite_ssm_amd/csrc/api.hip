@@ -6,6 +6,7 @@
 // shapes and alignment on the host before launching, so that no kernel is
 // launched on a shape it does not support.
 #include <cstring>
+#include <mutex>
 
 #include "internal.hpp"
 
@@ -321,6 +322,42 @@ int lssm_inproj_ssd_decode(lssm_ctx* ctx, const void* hidden, const void* norm_w
     return finish(ctx, "inproj_ssd_decode");
 }
 
+// ---------------------------------------------------------------------------
+// lssm_inproj_ssd_decode without a caller workspace and without allocating:
+// the projection's tagged words and the step tag live in `scratch`, a static
+// device array (zero at load, so no word carries a tag before its first use).
+// Its device address is looked up once per device with hipGetSymbolAddress;
+// host code uses only that address, never the array's name.  A one-thread
+// kernel advances the tag on the device before each fused launch, so every
+// call runs with a new tag and the host keeps no counter.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t NOALLOC_WORDS = 1u << 16;                 // projection rows it can carry
+constexpr size_t NOALLOC_BYTES = NOALLOC_WORDS * 8 + 256;  // words + the tag (512 KiB + 256 B)
+__device__ __align__(256) uint64_t scratch[NOALLOC_BYTES / 8];
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// This device's copy of `scratch` (the device must be current); null + error
+// text on failure.
+void* scratch_of(int dev) {
+    if (dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+__global__ void advance_tag_kernel(uint32_t* seq) {
+    if (threadIdx.x == 0) *seq += 1u;
+}
+}  // namespace
+
 int lssm_mixer_decode(lssm_ctx* ctx, void* hidden, const void* norm_w, const void* in_w,
                       const void* in_scales, void* conv_state, const void* conv_w,
                       const void* conv_b, const void* dt_bias, const void* A_log,
@@ -359,6 +396,57 @@ int lssm_mixer_decode(lssm_ctx* ctx, void* hidden, const void* norm_w, const voi
         return set_error(LSSM_EINVAL, "mixer_decode: shape, format, alignment or grid not supported by the fused launch");
     if (e != hipSuccess) return set_error(LSSM_EDEVICE, "mixer_decode: %s", hipGetErrorString(e));
     return finish(ctx, "mixer_decode");
+}
+
+int lssm_inproj_ssd_decode_noalloc(lssm_ctx* ctx, const void* hidden, const void* norm_w, const void* w,
+                                   const void* w_scales, void* conv_state, const void* conv_w,
+                                   const void* conv_b, const void* dt_bias, const void* A_log,
+                                   const void* D_skip, float* ssd_state, void* y, uint32_t d_model,
+                                   uint32_t d_inner, uint32_t d_state, uint32_t n_groups, uint32_t n_heads,
+                                   uint32_t d_head, uint32_t d_conv, float eps, lssm_wfmt wfmt,
+                                   lssm_dtype act) {
+    LSSM_CHECK_CTX(ctx);
+    LSSM_REQUIRE(valid_act(act), "inproj_ssd_decode_noalloc: unknown dtype");
+    if (int rc = check_fmt_k(d_model, wfmt, w_scales)) return rc;
+    LSSM_REQUIRE(ssd_state && y && norm_w && A_log && dt_bias, "inproj_ssd_decode_noalloc: null pointer");
+    LSSM_REQUIRE(n_heads >= 1 && n_groups >= 1 && d_inner == n_heads * d_head,
+                 "inproj_ssd_decode_noalloc: d_inner must equal n_heads * d_head");
+    const uint32_t xbc = d_inner + 2u * n_groups * d_state;
+    const size_t proj = (size_t)d_inner + xbc + n_heads;
+    LSSM_REQUIRE(proj <= NOALLOC_WORDS,
+                 "inproj_ssd_decode_noalloc: %zu projection rows exceed the static scratch of %zu rows", proj,
+                 NOALLOC_WORDS);
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
+        return set_error(LSSM_EINVAL, "inproj_ssd_decode_noalloc: the context's device must be current");
+    char* base = (char*)scratch_of(dev);
+    if (!base) return set_error(LSSM_EDEVICE, "inproj_ssd_decode_noalloc: hipGetSymbolAddress(scratch) failed");
+    uint64_t* words = reinterpret_cast<uint64_t*>(base);
+    uint32_t* seq = reinterpret_cast<uint32_t*>(base + NOALLOC_WORDS * 8);
+    InprojDecodeArgs a;
+    a.g = GemvArgs{hidden, d_model, w, w_scales, nullptr, 0, nullptr, norm_w, eps, 1u, (uint32_t)proj, d_model,
+                   wfmt, act, LSSM_EPI_NONE};
+    a.d_inner = d_inner;
+    a.xbc = xbc;
+    a.H = n_heads;
+    a.dconv = d_conv;
+    a.conv_state = conv_state;
+    a.conv_w = conv_w;
+    a.conv_b = conv_b;
+    a.z = nullptr;
+    a.xbc_act = nullptr;
+    a.dt = nullptr;
+    const SsdFuseArgs f{words, seq, 0u, ssd_state, A_log, dt_bias, D_skip, y, d_head, d_state, n_groups,
+                        1e-6f, 1e6f, ctx->status, 0u};
+    advance_tag_kernel<<<1, 64, 0, ctx->stream>>>(seq);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "inproj_ssd_decode_noalloc: %s", hipGetErrorString(e));
+    if (!launch_inproj_ssd_decode(ctx->stream, a, f, e))
+        return set_error(LSSM_EINVAL,
+                         "inproj_ssd_decode_noalloc: shape, format, alignment or grid not supported by the fused "
+                         "launch (the tag was advanced; the state was not touched)");
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "inproj_ssd_decode_noalloc: %s", hipGetErrorString(e));
+    return finish(ctx, "inproj_ssd_decode_noalloc");
 }
 
 int lssm_embed(lssm_ctx* ctx, const void* table, const int32_t* ids, void* out, uint32_t n,
