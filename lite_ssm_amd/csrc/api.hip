@@ -228,7 +228,42 @@ int lssm_ssd_chunked(lssm_ctx* ctx, const void* X, const void* B, const void* C,
     SsdArgs a{X, d.H * d.P, B, GN, C, GN, dt_raw, d.H, dt_bias, A_log, D_skip, Y, d.H * d.P, state,
               batch, d.L, d.H, d.P, d.N, d.n_groups, d.chunk_size, d.dt_min, d.dt_max, d.has_D, act,
               nullptr, 0};
-    hipError_t e = launch_ssd_chunked(ctx->stream, a);
+    // The context's workspaces: the segment workspace (allocated on first
+    // use) and the Gram tiles of the MFMA scan (grown on demand).  Neither is
+    // allocated while the stream is being captured; the scan then runs
+    // without them (unsegmented, each head forming its own C B^T).
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(ctx->stream, &cap);
+    if (e != hipSuccess) return set_error(LSSM_EDEVICE, "ssd_chunked: %s", hipGetErrorString(e));
+    if (cap == hipStreamCaptureStatusNone) {
+        if (!ctx->ssd_seg) {
+            e = hipMalloc((void**)&ctx->ssd_seg, ssd_seg_floats() * sizeof(float));
+            if (e != hipSuccess) {
+                ctx->ssd_seg = nullptr;
+                return set_error(LSSM_EDEVICE, "ssd_chunked: segment workspace: %s", hipGetErrorString(e));
+            }
+        }
+        const size_t gf = ssd_gram_floats(batch, d.L, d.n_groups);
+        if (act != LSSM_F32 && ctx->ssd_gram_cap < gf) {
+            if (ctx->ssd_gram) {
+                // the old tiles may still be read by launches in flight
+                e = hipStreamSynchronize(ctx->stream);
+                if (e == hipSuccess) e = hipFree(ctx->ssd_gram);
+                ctx->ssd_gram = nullptr;
+                ctx->ssd_gram_cap = 0;
+                if (e != hipSuccess) return set_error(LSSM_EDEVICE, "ssd_chunked: %s", hipGetErrorString(e));
+            }
+            e = hipMalloc((void**)&ctx->ssd_gram, gf * sizeof(float));
+            if (e != hipSuccess) {
+                ctx->ssd_gram = nullptr;
+                return set_error(LSSM_EDEVICE, "ssd_chunked: Gram workspace: %s", hipGetErrorString(e));
+            }
+            ctx->ssd_gram_cap = gf;
+        }
+    }
+    a.seg = ctx->ssd_seg;
+    if (act != LSSM_F32 && ctx->ssd_gram_cap >= ssd_gram_floats(batch, d.L, d.n_groups)) a.gram = ctx->ssd_gram;
+    e = launch_ssd_chunked(ctx->stream, a);
     if (e != hipSuccess) return set_error(LSSM_EDEVICE, "ssd_chunked: %s", hipGetErrorString(e));
     return finish(ctx, "ssd_chunked");
 }

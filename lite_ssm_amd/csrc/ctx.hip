@@ -125,6 +125,8 @@ int lssm_ctx_destroy(lssm_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(ctx->status);
     (void)hipHostFree(ctx->status_host);
+    if (ctx->ssd_seg) (void)hipFree(ctx->ssd_seg);
+    if (ctx->ssd_gram) (void)hipFree(ctx->ssd_gram);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return LSSM_OK;

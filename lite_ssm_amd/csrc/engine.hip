@@ -70,6 +70,7 @@ struct lssm_engine {
     float* ssd_state = nullptr;
     void* argmax_scratch = nullptr;
     float* gram = nullptr;     // prefill: the chunks' C B^T tiles, shared by a group's heads
+    float* seg = nullptr;      // prefill: the chunked scan's segment workspace
     // batch-1 decode: in_proj, the SSD step (and out_proj) in one launch
     // (tagged words of each layer's projection and gated SSD output; the tag
     // is a count of batch-1 steps the embedding advances, so consecutive uses
@@ -306,7 +307,7 @@ struct lssm_engine {
                               (char*)xbc_act + (size_t)(d_inner + GN) * es, xbc,
                               (char*)projb + (size_t)(d_inner + xbc) * es, proj, w.dt_bias, w.A_log, w.D,
                               ys, d_inner, ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act,
-                              nullptr, 0, gram};
+                              nullptr, 0, gram, seg};
                     e = launch_ssd_chunked(st(), s);
                 }
                 if (e == hipSuccess)
@@ -344,7 +345,7 @@ struct lssm_engine {
         if (e == hipSuccess) e = launch_conv1d_seed(st(), f_xbc, xbc, conv_layer(li), B, L, xbc, K, act);
         if (e == hipSuccess) {
             SsdArgs s{f_x, d_inner, f_B, GN, f_C, GN, f_dt, H, w.dt_bias, w.A_log, w.D, ys, d_inner,
-                      ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act, nullptr, 0};
+                      ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act, nullptr, 0, nullptr, seg};
             e = launch_ssd_chunked(st(), s);
         }
         if (e == hipSuccess)
@@ -480,6 +481,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A((void**)&e->ssd_state, (size_t)cfg->n_layer * max_batch * e->H * e->P * e->N * sizeof(float));
     A(&e->argmax_scratch, (size_t)max_batch * 128 * 8);
     A((void**)&e->gram, ssd_gram_floats(max_batch, max_seq, G) * sizeof(float));
+    A((void**)&e->seg, ssd_seg_floats() * sizeof(float));
     if (e->short_fused()) {
         const size_t R16 = (size_t)max_batch * 16;
         A(&e->f_z, R16 * d_inner * es);

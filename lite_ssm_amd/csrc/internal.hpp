@@ -26,6 +26,12 @@ struct lssm_ctx {
     uint32_t* status = nullptr;
     uint32_t* status_host = nullptr;
     uint32_t debug = 0;      // LSSM_DEBUG_* switches (lssm_ctx_set_debug)
+    // segment workspace of the chunked scan (lssm::ssd_seg_floats() floats),
+    // allocated by the first lssm_ssd_chunked call that can use it
+    float* ssd_seg = nullptr;
+    // Gram tiles of lssm_ssd_chunked (lssm::ssd_gram_floats), grown on demand
+    float* ssd_gram = nullptr;
+    size_t ssd_gram_cap = 0;   // floats
 };
 
 namespace lssm {
@@ -172,12 +178,25 @@ struct SsdArgs {
     // the chunks' C B^T Gram tiles, computed once per (sequence, chunk, group)
     // and shared by the group's heads (null: every head computes its own)
     float* gram = nullptr;
+    // chunked scan, optional: workspace of ssd_seg_floats() floats with which
+    // a grid of fewer blocks than the chip holds splits every sequence into
+    // segments of chunks that run in parallel (null: one serial walk per
+    // sequence, head and column block)
+    float* seg = nullptr;
+    // set by the launcher: segments per sequence and chunks per segment
+    uint32_t nseg = 1, seg_chunks = 0;
 };
 hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a);
 hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a);
 inline size_t ssd_gram_floats(uint32_t batch, uint32_t L, uint32_t G) {
     return (size_t)batch * ((L + 63) / 64) * G * 64 * 64;
 }
+// Segment workspace: the states of [batch][segment][H][P][N] (fp32) and the
+// segments' log-decays [batch][segment][H]; the launcher takes only as many
+// segments as fit.
+constexpr size_t SSD_SEG_STATE_FLOATS = (size_t)512 * 64 * 128;   // 16 MiB
+constexpr size_t SSD_SEG_DECAY_FLOATS = 4096;
+inline size_t ssd_seg_floats() { return SSD_SEG_STATE_FLOATS + SSD_SEG_DECAY_FLOATS; }
 
 hipError_t launch_inproj_fused(hipStream_t s, const void* normed, const void* W_in,
                                const void* W_conv, const void* conv_b, void* proj_z, void* ssd_x,

@@ -9,6 +9,7 @@
 //   S[p,n] = r(e^{L_end} S[p,n] + sum_j e^{L_end - Lcum_j} DT_j B[j,n] X[j,p])
 // with S held in the activation dtype between chunks (the reference keeps it
 // in `half` threadgroup memory) and written back as fp32.
+#include <algorithm>
 #include <cfloat>
 #include <cstdlib>
 
@@ -334,8 +335,11 @@ __global__ __launch_bounds__(256) void ssd_gram_kernel(SsdArgs a) {
 // the halves trade their updated state tiles through LDS at the mid-chunk
 // barrier.  The serial chain per chunk is then about half as long, and a CU
 // holds twice the waves.
+// (four-wave blocks are held to 256 registers, two blocks per CU: a grid
+// slightly larger than the CU count runs in one round)
 template <typename T, int NW, bool GP, int SPL>
-__global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a) {
+__global__ __launch_bounds__(64 * NW * SPL) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 2 : 1)))
+void ssd_chunk_mfma_kernel(SsdArgs a) {
     constexpr int NWV = NW * SPL;         // waves
     constexpr int NT = 64 * NWV;          // threads
     constexpr int PB = 16 * NW;           // state columns p per block
@@ -368,6 +372,13 @@ __global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a
     const T* dtr = (const T*)a.dt + (size_t)b * L * a.dt_stride + h;
     T* Y = (T*)a.Y + (size_t)b * L * a.y_stride + (size_t)h * P + p0;
     float* st = a.state + (((size_t)b * H + h) * P + p0) * CN;
+    // segment blockIdx.z of a.nseg: chunks cb .. ce - 1, starting from the
+    // state the segment pass left in the workspace; only the last segment
+    // writes the final state
+    const uint32_t sg = blockIdx.z, nchs = (L + CQ - 1) / CQ;
+    const uint32_t cb = sg * a.seg_chunks, ce = min(nchs, cb + a.seg_chunks);
+    const bool last_seg = sg + 1 == a.nseg;
+    const float* st_in = a.nseg > 1 ? a.seg + ((((size_t)b * a.nseg + sg) * H + h) * P + p0) * CN : st;
     const float A_h = -expf(to_f(((const T*)a.A_log)[h]));
     const float dt_b = to_f(((const T*)a.dt_bias)[h]);
     const float D_h = a.has_D ? to_f(((const T*)a.D)[h]) : 0.0f;
@@ -384,7 +395,7 @@ __global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a
     s4v sp[8];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
-        sp[nt] = pack4<T>(*reinterpret_cast<const floatx4*>(st + (size_t)(pw + li) * CN + 16 * nt + 4 * lq));
+        sp[nt] = pack4<T>(*reinterpret_cast<const floatx4*>(st_in + (size_t)(pw + li) * CN + 16 * nt + 4 * lq));
 
     // D x as one more MFMA: X^T times the diagonal tile D I (exact in T).
     // Token tile Tt lies in k-slice Tt / 2, where column t = 16 Tt + li has its
@@ -485,20 +496,20 @@ __global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a
         Wb[buf][lane] = __expf(l_end - v) * dv;
     };
 
-    const uint32_t nch = (L + CQ - 1) / CQ;
-    fetch(0);
+    fetch(cb * CQ);
     stage();
-    if (w == 0) scan(0, 0);
-    if (nch > 1) fetch(CQ);
+    if (w == 0) scan(cb * CQ, 0);
+    if (cb + 1 < ce) fetch((cb + 1) * CQ);
     __syncthreads();
 
-    for (uint32_t c = 0; c < nch; ++c) {
+    for (uint32_t c = cb; c < ce; ++c) {
+        const uint32_t par = (c - cb) & 1;   // buffer of this chunk's scalars
         const uint32_t t0 = c * CQ;
         const uint32_t tl = min((uint32_t)CQ, L - t0);
 
-        const float* LCs = LCb[c & 1];
-        const float* ELs = ELb[c & 1];
-        const float* Ws = Wb[c & 1];
+        const float* LCs = LCb[par];
+        const float* ELs = ELb[par];
+        const float* Ws = Wb[par];
 
         // ---- G^T tiles (J <= T) -> M.  Twelve tiles, wave w takes positions
         // w, w + NW, ...; positions 0 and 4 are the zero upper halves (1,0)
@@ -507,7 +518,7 @@ __global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a
         // an immediate (an indexed array would be a memory load whose wait
         // would also wait for the prefetch). ----
         {
-            const float* DTs = DTb[c & 1];
+            const float* DTs = DTb[par];
 #pragma unroll
             for (int i = 0; i < NTL; ++i) {
                 const int kt = w + NWV * i;
@@ -546,7 +557,7 @@ __global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a
                 *reinterpret_cast<s4v*>(Ms + t * MPAD + 16 * J + 4 * lq) = m4;
             }
         }
-        if (w == 0 && c + 1 < nch) scan(t0 + CQ, (c + 1) & 1);
+        if (w == 0 && c + 1 < ce) scan(t0 + CQ, par ^ 1);
 
         // ---- X^T slices of this wave's columns (k = token) ----
         s8v xf[2];
@@ -618,7 +629,7 @@ __global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a
         // Stage the next chunk first: its loads were issued a chunk ago, and
         // waiting for them before the Y stores below keeps those stores out
         // of the wait.
-        if (c + 1 < nch) stage();
+        if (c + 1 < ce) stage();
 
         // ---- Y^T += X^T M^T + X^T (D I), store ----
 #pragma unroll
@@ -635,15 +646,192 @@ __global__ __launch_bounds__(64 * NW * SPL) void ssd_chunk_mfma_kernel(SsdArgs a
             if ((uint32_t)t < tl)
                 *reinterpret_cast<s4v*>(Y + (size_t)(t0 + t) * a.y_stride + pw + 4 * lq) = pack4<T>(yacc[Tt]);
         }
-        if (c + 2 < nch) fetch(t0 + 2 * CQ);
+        if (c + 2 < ce) fetch(t0 + 2 * CQ);
         __syncthreads();
     }
+    if (!last_seg) return;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
         if (nt / NST == hh)
             *reinterpret_cast<floatx4*>(st + (size_t)(pw + li) * CN + 16 * nt + 4 * lq) = unpack4<T>(sp[nt]);
 }
 
+
+// ---------------------------------------------------------------------------
+// Segmented chunked scan.  When a grid of (sequence, head, column block)
+// walks would leave CUs idle, each sequence's chunks are split into a.nseg
+// segments of a.seg_chunks chunks, run in three launches:
+//   1. ssd_seg_state_kernel, segments 0 .. nseg - 2 in parallel: the state
+//      the segment's chunks leave when it starts from zero,
+//        S_s = sum_c e^{sum of L_end after c} B_c^T (w_c o X_c)   (fp32),
+//      by the walk's state update without its rounding, and the segment's
+//      log-decay sum_c L_end(c);
+//   2. ssd_seg_scan_kernel: the state entering every segment,
+//        S_in(0) = S_init,  S_in(s + 1) = e^{decay(s)} S_in(s) + S_s,
+//      in place over the workspace (an exact recurrence over nseg terms);
+//   3. the walk, all segments at once, segment s from S_in(s) (rounded to
+//      the activation type as the walk holds its state); the last segment
+//      writes the final state.
+// The walk rounds its state after every chunk as ssd_chunked.metal does;
+// across a segment boundary the entering state is the fp32 recurrence
+// instead of the chain of rounded states, so results agree with the
+// unsegmented scan to within that rounding.
+// ---------------------------------------------------------------------------
+template <typename T, int NW>
+__global__ __launch_bounds__(64 * NW) void ssd_seg_state_kernel(SsdArgs a) {
+    constexpr int NT = 64 * NW;
+    constexpr int PB = 16 * NW;           // state columns p per block
+    constexpr int XP = PB + 8;            // X row pitch
+    constexpr int BV = CQ * CN / 8 / NT;  // 16-byte pieces of B per thread
+    constexpr int XV = CQ * PB / 8 / NT;  // 16-byte pieces of X per thread
+    constexpr int BR = NT / 16, XR = NT / (PB / 8);
+    // double-buffered: chunk c + 1 is staged while chunk c is in use, so one
+    // barrier per chunk
+    __shared__ __attribute__((aligned(16))) T Bs[2][CQ * SPAD];
+    __shared__ __attribute__((aligned(16))) T Xs[2][CQ * XP];
+    __shared__ __attribute__((aligned(16))) float Wb[2][CQ];
+    __shared__ float LEb[2];
+
+    const uint32_t P = a.P, H = a.H, L = a.L;
+    const uint32_t npb = P / PB;
+    const uint32_t h = blockIdx.x / npb, pb = blockIdx.x % npb, b = blockIdx.y, sg = blockIdx.z;
+    const uint32_t p0 = pb * PB;
+    const uint32_t hpg = (H / a.G) > 0 ? H / a.G : 1;
+    const uint32_t g = h / hpg;
+    const uint32_t nch = (L + CQ - 1) / CQ;
+    const uint32_t cb = sg * a.seg_chunks, ce = min(nch, cb + a.seg_chunks);
+    const T* X = (const T*)a.X + (size_t)b * L * a.x_stride + (size_t)h * P + p0;
+    const T* Bv = (const T*)a.B + (size_t)b * L * a.b_stride + (size_t)g * CN;
+    const T* dtr = (const T*)a.dt + (size_t)b * L * a.dt_stride + h;
+    const float A_h = -expf(to_f(((const T*)a.A_log)[h]));
+    const float dt_b = to_f(((const T*)a.dt_bias)[h]);
+
+    const int tid = threadIdx.x;
+    const int lane = tid % WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int li = lane % 16, lq = lane / 16;
+    const int tk = li / 4, tc = li % 4;
+    const int pw = 16 * w;
+
+    const uint32_t brow = tid / 16, bcol = (tid % 16) * 8;
+    const uint32_t xrow = tid / (PB / 8), xcol = (tid % (PB / 8)) * 8;
+    u32x4 rb[BV], rx[XV];
+    uint32_t rdt = 0;
+    // rows past L (last chunk) re-read row t0; their state weight is 0
+    auto fetch = [&](uint32_t t0) {
+        const uint32_t tl = min((uint32_t)CQ, L - t0);
+#pragma unroll
+        for (int v = 0; v < BV; ++v) {
+            const uint32_t t = brow + BR * v, tt = t0 + (t < tl ? t : 0);
+            rb[v] = *reinterpret_cast<const u32x4*>(Bv + (size_t)tt * a.b_stride + bcol);
+        }
+#pragma unroll
+        for (int v = 0; v < XV; ++v) {
+            const uint32_t t = xrow + XR * v, tt = t0 + (t < tl ? t : 0);
+            rx[v] = *reinterpret_cast<const u32x4*>(X + (size_t)tt * a.x_stride + xcol);
+        }
+        if (w == 0) rdt = raw_of(dtr + (size_t)(t0 + min((uint32_t)lane, tl - 1)) * a.dt_stride);
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int v = 0; v < BV; ++v) *reinterpret_cast<u32x4*>(Bs[buf] + (brow + BR * v) * SPAD + bcol) = rb[v];
+#pragma unroll
+        for (int v = 0; v < XV; ++v) *reinterpret_cast<u32x4*>(Xs[buf] + (xrow + XR * v) * XP + xcol) = rx[v];
+    };
+    // wave 0: the state weights w and L_end of the chunk at t0, as the walk's
+    // scan computes them
+    auto scan = [&](uint32_t t0, int buf) {
+        const uint32_t tl = min((uint32_t)CQ, L - t0);
+        float dv = 0.0f;
+        if ((uint32_t)lane < tl) {
+            dv = softplus_f(f_of<T>(rdt) + dt_b);
+            dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
+        }
+        float v = A_h * dv;
+#pragma unroll
+        for (int off = 1; off < WAVE; off <<= 1) {
+            const float o = __shfl_up(v, off, WAVE);
+            if (lane >= off) v += o;
+        }
+        const float l_end = __shfl(v, WAVE - 1, WAVE);
+        Wb[buf][lane] = __expf(l_end - v) * dv;
+        if (lane == 0) LEb[buf] = l_end;
+    };
+
+    floatx4 sf[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) sf[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float lseg = 0.0f;
+    fetch(cb * CQ);
+    for (uint32_t c = cb; c < ce; ++c) {
+        const int buf = (c - cb) & 1;
+        stage(buf);
+        if (w == 0) scan(c * CQ, buf);
+        __syncthreads();
+        if (c + 1 < ce) fetch((c + 1) * CQ);
+        const float le = LEb[buf];
+        lseg += le;
+        const float dch = __expf(le);
+        s8v xf[2], wx[2];
+#pragma unroll
+        for (int ka = 0; ka < 2; ++ka) {
+            const T* xp = Xs[buf] + (32 * ka + 8 * lq + tk) * XP + pw + 4 * tc;
+            xf[ka] = cat8(ld_tr(xp), ld_tr(xp + 4 * XP));
+            const floatx4 w0 = *reinterpret_cast<const floatx4*>(Wb[buf] + 32 * ka + 8 * lq);
+            const floatx4 w1 = *reinterpret_cast<const floatx4*>(Wb[buf] + 32 * ka + 8 * lq + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wx[ka][e] = bits_of<T>(w0[e] * val_of<T>(xf[ka][e]));
+                wx[ka][e + 4] = bits_of<T>(w1[e] * val_of<T>(xf[ka][e + 4]));
+            }
+        }
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+            floatx4 acc = sf[nt];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] *= dch;
+#pragma unroll
+            for (int ka = 0; ka < 2; ++ka) {
+                const T* bp = Bs[buf] + (32 * ka + 8 * lq + tk) * SPAD + 16 * nt + 4 * tc;
+                acc = mma16<T>(cat8(ld_tr(bp), ld_tr(bp + 4 * SPAD)), wx[ka], acc);
+            }
+            sf[nt] = acc;
+        }
+    }
+    float* out = a.seg + ((((size_t)b * a.nseg + sg) * H + h) * P + p0) * CN;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+        *reinterpret_cast<floatx4*>(out + (size_t)(pw + li) * CN + 16 * nt + 4 * lq) = sf[nt];
+    if (pb == 0 && tid == 0)
+        a.seg[(size_t)a.batch * a.nseg * H * P * CN + ((size_t)b * a.nseg + sg) * H + h] = lseg;
+}
+
+// S_in(s) for every segment, in place over the workspace (thread: 4
+// consecutive state entries of one sequence).  Slot s holds S_s from the
+// segment pass (s < nseg - 1) and receives S_in(s).
+__global__ __launch_bounds__(256) void ssd_seg_scan_kernel(SsdArgs a) {
+    const size_t per_b = (size_t)a.H * a.P * CN;
+    const size_t i = 4 * ((size_t)blockIdx.x * 256 + threadIdx.x);
+    if (i >= (size_t)a.batch * per_b) return;
+    const uint32_t b = (uint32_t)(i / per_b);
+    const size_t r = i % per_b;
+    const uint32_t h = (uint32_t)(r / ((size_t)a.P * CN));
+    const uint32_t ns = a.nseg;
+    const float* dec = a.seg + (size_t)a.batch * ns * per_b;
+    floatx4 v = *reinterpret_cast<const floatx4*>(a.state + i);
+    for (uint32_t s = 0; s < ns; ++s) {
+        floatx4* slot = reinterpret_cast<floatx4*>(a.seg + ((size_t)b * ns + s) * per_b + r);
+        if (s + 1 < ns) {
+            const floatx4 loc = *slot;
+            *slot = v;
+            const float d = __expf(dec[((size_t)b * ns + s) * a.H + h]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = d * v[e] + loc[e];
+        } else {
+            *slot = v;
+        }
+    }
+}
 
 // ---------------------------------------------------------------------------
 // Chunked scan for fp32 activations on v_mfma_f32_16x16x4_f32 (chunk 64,
@@ -673,6 +861,8 @@ __device__ __forceinline__ floatx4 mma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// LOCAL: the segment pass of the segmented scan (state from zero, no Y).
+template <bool LOCAL>
 __global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
     __shared__ float Cs[CQ * F_CP];
     __shared__ float Bs[CQ * F_BP];
@@ -692,6 +882,10 @@ __global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
     const float* dtr = (const float*)a.dt + (size_t)b * L * a.dt_stride + h;
     float* Y = (float*)a.Y + (size_t)b * L * a.y_stride + (size_t)h * P + p0;
     float* st = a.state + (((size_t)b * H + h) * P + p0) * CN;
+    // segment blockIdx.z: chunks cb .. ce - 1 (one segment: all chunks)
+    const uint32_t sg = blockIdx.z, nch = (L + CQ - 1) / CQ;
+    const uint32_t cb = sg * a.seg_chunks, ce = min(nch, cb + a.seg_chunks);
+    float* seg_slot = a.nseg > 1 ? a.seg + ((((size_t)b * a.nseg + sg) * H + h) * P + p0) * CN : nullptr;
     const float A_h = -expf(((const float*)a.A_log)[h]);
     const float dt_b = ((const float*)a.dt_bias)[h];
     const float D_h = a.has_D ? ((const float*)a.D)[h] : 0.0f;
@@ -703,17 +897,19 @@ __global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
 
     // S^T tiles: sT[nt][r] = S[p = pw + li][n = f_srow(nt, 4 lq + r)] (4 consecutive n)
     floatx4 sT[8];
+    const float* st_in = seg_slot ? seg_slot : st;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
-        sT[nt] = *reinterpret_cast<const floatx4*>(st + (size_t)(pw + li) * CN + f_srow(nt, 4 * lq));
+        sT[nt] = LOCAL ? floatx4{0.0f, 0.0f, 0.0f, 0.0f}
+                       : *reinterpret_cast<const floatx4*>(st_in + (size_t)(pw + li) * CN + f_srow(nt, 4 * lq));
+    float lseg = 0.0f;
 
-    const uint32_t nch = (L + CQ - 1) / CQ;
-    for (uint32_t c = 0; c < nch; ++c) {
+    for (uint32_t c = cb; c < ce; ++c) {
         const uint32_t t0 = c * CQ, tl = min((uint32_t)CQ, L - t0);
         // ---- stage the chunk (rows past tl as zeros) and scan DT / Lcum ----
         for (uint32_t i = tid; i < CQ * CN; i += 256) {
             const uint32_t t = i / CN, n = i % CN;
-            Cs[t * F_CP + n] = t < tl ? Cv[(size_t)(t0 + t) * a.c_stride + n] : 0.0f;
+            if (!LOCAL) Cs[t * F_CP + n] = t < tl ? Cv[(size_t)(t0 + t) * a.c_stride + n] : 0.0f;
             Bs[t * F_BP + n] = t < tl ? Bv[(size_t)(t0 + t) * a.b_stride + n] : 0.0f;
         }
         for (uint32_t i = tid; i < CQ * 64; i += 256) {
@@ -739,8 +935,9 @@ __global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
             Ws[lane] = expf(l_end - v) * dv;
         }
         __syncthreads();
+        if (LOCAL) lseg += LCs[CQ - 1];
         // ---- M = G e^{Lc_t - Lc_j} DT_j on the ten lower tiles (J <= T) ----
-        for (int kt = w; kt < 10; kt += 4) {
+        for (int kt = w; kt < (LOCAL ? 0 : 10); kt += 4) {
             constexpr uint64_t JT = 0x0ull | 0x4ull << 4 | 0x5ull << 8 | 0x8ull << 12 | 0x9ull << 16 |
                                     0xAull << 20 | 0xCull << 24 | 0xDull << 28 | 0xEull << 32 | 0xFull << 36;
             const int jt = (int)(JT >> (4 * kt)) & 15;
@@ -761,10 +958,10 @@ __global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
                 Ms[t * F_MP + j] = (j <= t && (uint32_t)t < tl) ? mv : 0.0f;
             }
         }
-        __syncthreads();   // (token tile Tt reads M columns j < 16 (Tt + 1) only)
+        if (!LOCAL) __syncthreads();   // (token tile Tt reads M columns j < 16 (Tt + 1) only)
         // ---- Y^T for this wave's columns ----
 #pragma unroll
-        for (int Tt = 0; Tt < 4; ++Tt) {
+        for (int Tt = 0; Tt < (LOCAL ? 0 : 4); ++Tt) {
             floatx4 yo = {0.0f, 0.0f, 0.0f, 0.0f};
             const float* cr = Cs + (16 * Tt + li) * F_CP;
 #pragma unroll
@@ -804,9 +1001,16 @@ __global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
         }
         __syncthreads();   // staging and M no longer read
     }
+    if (LOCAL) {
+        if (pb == 0 && tid == 0)
+            a.seg[(size_t)a.batch * a.nseg * H * P * CN + ((size_t)b * a.nseg + sg) * H + h] = lseg;
+    } else if (sg + 1 != a.nseg) {
+        return;
+    }
+    float* out = LOCAL ? seg_slot : st;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
-        *reinterpret_cast<floatx4*>(st + (size_t)(pw + li) * CN + f_srow(nt, 4 * lq)) = sT[nt];
+        *reinterpret_cast<floatx4*>(out + (size_t)(pw + li) * CN + f_srow(nt, 4 * lq)) = sT[nt];
 }
 
 template <typename T, bool GATE>
@@ -834,8 +1038,33 @@ hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a) {
     return gate ? step_go<float, true>(s, a) : step_go<float, false>(s, a);
 }
 
-hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a) {
-    if (a.batch == 0 || a.H == 0 || a.L == 0) return hipSuccess;
+// Segments per sequence of the chunked scan: enough for about two blocks per
+// CU when the (sequence, head, column block) walks alone would leave CUs
+// idle, as many as the workspace holds, none without a workspace.
+// LSSM_SSD_SEGMENTS overrides the count (read once).
+static uint32_t pick_segments(const SsdArgs& a, size_t nblk0) {
+    const uint32_t nch = (a.L + CQ - 1) / CQ;
+    if (!a.seg || nch < 2) return 1;
+    static const int env = [] {
+        const char* e = getenv("LSSM_SSD_SEGMENTS");
+        return e ? atoi(e) : 0;
+    }();
+    const size_t cus = num_cus();
+    size_t ns = env > 0 ? (size_t)env : (nblk0 >= cus ? 1 : (2 * cus + nblk0 - 1) / nblk0);
+    ns = std::min(ns, (size_t)nch);
+    const size_t per = (size_t)a.batch * a.H * a.P * CN;   // floats of one segment slot, all sequences
+    while (ns > 1 && (ns * per > SSD_SEG_STATE_FLOATS || ns * a.batch * a.H > SSD_SEG_DECAY_FLOATS)) --ns;
+    if (ns <= 1) return 1;
+    const uint32_t K = (nch + (uint32_t)ns - 1) / (uint32_t)ns;
+    return (nch + K - 1) / K;                              // no empty segment
+}
+
+hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a0) {
+    if (a0.batch == 0 || a0.H == 0 || a0.L == 0) return hipSuccess;
+    SsdArgs a = a0;
+    const uint32_t nch = (a.L + CQ - 1) / CQ;
+    a.nseg = 1;
+    a.seg_chunks = nch;
     // A single partial chunk (L < 64, chunk == L) has the same rounding points
     // as chunk 64, so it also takes the MFMA path.
     const bool chunk_ok = a.chunk == CQ || (a.chunk == a.L && a.L < CQ);
@@ -844,25 +1073,42 @@ hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a) {
                          (a.y_stride % 4 == 0) && ((uintptr_t)a.X % 16 == 0) &&
                          ((uintptr_t)a.B % 16 == 0) && ((uintptr_t)a.C % 16 == 0) &&
                          ((uintptr_t)a.Y % 8 == 0) && ((uintptr_t)a.state % 16 == 0);
+    const size_t cus = num_cus();
+    // segment pass + the scan of the segments' states (a.nseg > 1)
+    auto seg_scan = [&]() {
+        const size_t n4 = (size_t)a.batch * a.H * a.P * CN / 4;
+        ssd_seg_scan_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(a);
+    };
     if (mfma_ok) {
         // Four waves (64 columns of P) per block when that still gives a
-        // block per CU; otherwise two, for more blocks.
-        const bool nw4 = (a.P % 64) == 0 && (size_t)a.batch * a.H * (a.P / 64) >= (size_t)num_cus();
+        // block per CU, or when segments make up the count; otherwise two,
+        // for more blocks.
+        const size_t nb64 = (size_t)a.batch * a.H * (a.P / 64);
+        const bool p64 = (a.P % 64) == 0;
+        const bool nw4 = p64 && (nb64 >= cus || (a.seg && nch >= 2));
+        const uint32_t pbw = nw4 ? 64 : 32;
+        a.nseg = pick_segments(a, (size_t)a.batch * a.H * (a.P / pbw));
+        a.seg_chunks = (nch + a.nseg - 1) / a.nseg;
         const bool gp = a.gram != nullptr;
         auto go = [&](auto tag) {
             using T = decltype(tag);
             if (gp) {
-                const dim3 gg((a.L + CQ - 1) / CQ, a.G, a.batch);
+                const dim3 gg(nch, a.G, a.batch);
                 ssd_gram_kernel<T><<<gg, 256, 0, s>>>(a);
+            }
+            if (a.nseg > 1) {
+                if (p64) ssd_seg_state_kernel<T, 4><<<dim3(a.H * (a.P / 64), a.batch, a.nseg - 1), 256, 0, s>>>(a);
+                else ssd_seg_state_kernel<T, 2><<<dim3(a.H * (a.P / 32), a.batch, a.nseg - 1), 128, 0, s>>>(a);
+                seg_scan();
             }
             // two waves per 16-column slice (SPL = 2) when the grid does not
             // fill the chip anyway (then every block has a CU to itself and
             // the shorter chain wins; with more blocks than CUs the larger
             // register footprint of SPL = 2 costs a second round of blocks)
-            const size_t nblk = (size_t)a.batch * a.H * (a.P / (nw4 ? 64 : 32));
-            const bool split = nblk <= (size_t)num_cus();
+            const size_t nblk = (size_t)a.batch * a.H * (a.P / pbw) * a.nseg;
+            const bool split = nblk <= cus;
+            const dim3 grid(a.H * (a.P / pbw), a.batch, a.nseg);
             if (nw4) {
-                const dim3 grid(a.H * (a.P / 64), a.batch);
                 if (split) {
                     if (gp) ssd_chunk_mfma_kernel<T, 4, true, 2><<<grid, 512, 0, s>>>(a);
                     else ssd_chunk_mfma_kernel<T, 4, false, 2><<<grid, 512, 0, s>>>(a);
@@ -871,7 +1117,6 @@ hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a) {
                     else ssd_chunk_mfma_kernel<T, 4, false, 1><<<grid, 256, 0, s>>>(a);
                 }
             } else {
-                const dim3 grid(a.H * (a.P / 32), a.batch);
                 if (split) {
                     if (gp) ssd_chunk_mfma_kernel<T, 2, true, 2><<<grid, 256, 0, s>>>(a);
                     else ssd_chunk_mfma_kernel<T, 2, false, 2><<<grid, 256, 0, s>>>(a);
@@ -887,7 +1132,13 @@ hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a) {
     }
     if (a.act == LSSM_F32 && chunk_ok && a.N == CN && (a.P % 64) == 0 && ((uintptr_t)a.state % 16 == 0) &&
         ((uintptr_t)a.Y % 16 == 0) && (a.y_stride % 4 == 0)) {
-        ssd_chunk_f32_mfma_kernel<<<dim3(a.H * (a.P / 64), a.batch), 256, 0, s>>>(a);
+        a.nseg = pick_segments(a, (size_t)a.batch * a.H * (a.P / 64));
+        a.seg_chunks = (nch + a.nseg - 1) / a.nseg;
+        if (a.nseg > 1) {
+            ssd_chunk_f32_mfma_kernel<true><<<dim3(a.H * (a.P / 64), a.batch, a.nseg - 1), 256, 0, s>>>(a);
+            seg_scan();
+        }
+        ssd_chunk_f32_mfma_kernel<false><<<dim3(a.H * (a.P / 64), a.batch, a.nseg), 256, 0, s>>>(a);
         return hipGetLastError();
     }
     if (a.chunk > (uint32_t)SC_MAXCK || a.N > (uint32_t)SC_MAXN) return hipErrorInvalidValue;

@@ -339,7 +339,7 @@ def test_ssd_chunked_config1_fp32(ctx, rng):
 
 
 @pytest.mark.parametrize("batch,Lq,H,G,P", [(1, 512, 24, 1, 64), (2, 200, 8, 2, 128), (1, 40, 4, 1, 64),
-                                            (3, 64, 16, 8, 64)])
+                                            (3, 64, 16, 8, 64), (1, 1950, 24, 1, 64)])
 def test_ssd_chunked_fp32_mfma_vs_oracle(ctx, rng, batch, Lq, H, G, P):
     """The fp32 chunked scan on v_mfma_f32_16x16x4_f32: a nonzero initial
     state, ragged last chunks, several groups and P slices, max-rel 1e-3 on y
@@ -358,12 +358,15 @@ def test_ssd_chunked_fp32_mfma_vs_oracle(ctx, rng, batch, Lq, H, G, P):
     assert max_rel(host(sd, np.float32), s2) < 1e-3
 
 
-# (4, 130, 64, 1) and P = 128 give at least one block per CU with four waves
-# per block (64 state columns); the others take the two-wave blocks.
+# Grids of fewer blocks than CUs run segmented (the sequence's chunks split
+# into segments that run in parallel): (1, 512, 24) one chunk per segment,
+# (1, 1950, 24) two per segment and a last segment of one partial chunk.
+# (4, 130, 64, 1) and P = 128 give at least one block per CU and run
+# unsegmented; P = 32 takes the two-wave blocks.
 @pytest.mark.parametrize("act", [O.F16, O.BF16])
 @pytest.mark.parametrize("batch,Lq,H,G,P", [(1, 512, 24, 1, 64), (2, 200, 8, 2, 64), (1, 40, 4, 1, 64),
                                             (3, 64, 16, 8, 64), (4, 130, 64, 1, 64), (2, 100, 6, 2, 32),
-                                            (2, 150, 128, 1, 128)])
+                                            (2, 150, 128, 1, 128), (1, 1950, 24, 1, 64)])
 def test_ssd_chunked_mfma_vs_oracle(ctx, rng, act, batch, Lq, H, G, P):
     L = _lib()
     N = 128
