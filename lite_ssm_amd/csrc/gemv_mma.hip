@@ -2,6 +2,7 @@
 // (exact dequantization, linear.metal:440-474), RMSNorm prologue and the
 // per-row epilogues of gemv.hip fused.
 #include <algorithm>
+#include <cstdlib>
 
 #include "gemv_core.cuh"
 
@@ -507,6 +508,247 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
     }
 }
 
+// ---------------------------------------------------------------------------
+// gemv_mmx: the gemv_mma product for x packed by launch_mma_pack, 2..32 rows
+// in one pass (RT = 1 or 2 tiles of 16 batch rows), int4 group 64 x bf16
+// (the 2.7B / 8B decode linears).  Nothing is staged: the A fragments are
+// read straight from the packed rows (at most 32 rows of K / 2 dwords, which
+// stay in L2), and every unpacked weight slice meets all RT row tiles.  A
+// wave requests the x of its first two quads, then all its weights and
+// scales (one round trip to HBM per block), then, while it works through the
+// quads, the x of the quad two ahead.  (A wave's loads complete in the order
+// they were issued: x requested behind the weights could not be used before
+// every weight had arrived.)  The LDS holds only the KS partial sums, and a
+// block owns up to three tiles of 16 W rows so that the grid is about one
+// block per CU.  Per wave, the k-slices and the group scaling are
+// gemv_mma_kernel's and the partials are summed in wave order; the K split
+// (at most 8 waves here) can differ from that kernel's, so the two may round
+// the fp32 sum of an output differently.
+// ---------------------------------------------------------------------------
+constexpr int MMX_MAXW = 8;                      // waves per block: the K split
+
+template <int FMT, typename T, int CT, int RT, int QPW, class Epi>
+__global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi epi, uint32_t M) {
+    using P = Mma<FMT, T>;
+    using F = Fmt<FMT, T>;
+    constexpr int NP = P::NP, GPQ = P::GPQ, SPG = P::SPG, SPQ = P::SPQ;
+    constexpr bool BIAS = P::BIAS;
+    static_assert(P::G > 0 && GPQ == 2, "int4 group 64");
+    extern __shared__ __attribute__((aligned(16))) uint32_t mm_lds[];
+
+    const uint32_t K = c.K, N = c.N, KH = K / 2;
+    const int lane = threadIdx.x % WAVE, li = lane % 16, lq = lane / 16;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    const uint32_t KS = blockDim.x / WAVE;
+    const uint32_t qa0 = w * QPW;
+    const uint32_t tiles = (N + 15) / 16, tile0 = blockIdx.x * CT;
+    const size_t rb = F::row_bytes(K);
+    epi.pin();
+
+    const uint32_t* xrow[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) xrow[rt] = c.xp + (size_t)min(16u * rt + li, M - 1) * KH;
+    u32x4 xr[2][RT][SPQ];                                      // x of two quads
+    auto load_x = [&](int qd, u32x4 (&xb)[RT][SPQ]) {
+        const uint32_t qa = qa0 + qd;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int sl = 0; sl < SPQ; ++sl) {
+                int ch, po;
+                mma_slice_pos<FMT>(sl, lq, ch, po);
+                xb[rt][sl] = *reinterpret_cast<const u32x4*>(xrow[rt] + (4 * qa + ch) * NP + po);
+            }
+    };
+    load_x(0, xr[0]);
+    if (QPW > 1) load_x(1, xr[1]);
+    // all weights and scales of the wave's quads
+    u32x4 wr[QPW][CT];
+    uint32_t sr[QPW][CT];                                      // the quad's two group scales
+#pragma unroll
+    for (int t = 0; t < CT; ++t) {
+        const uint32_t n = min(16 * (tile0 + t) + li, N - 1);
+        const uint8_t* wp = c.w + n * rb + 16 * lq;
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(c.s + (size_t)n * (K / P::G));
+#pragma unroll
+        for (int qd = 0; qd < QPW; ++qd) {
+            wr[qd][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp + 64 * (qa0 + qd)));
+            sr[qd][t] = sp[qa0 + qd];
+        }
+    }
+
+    floatx4 acc[RT][CT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int t = 0; t < CT; ++t) acc[rt][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute_q = [&](const u32x4 (&wb)[CT], const uint32_t (&sb)[CT], const u32x4 (&xb)[RT][SPQ]) {
+        // the 4 lanes of each row trade dwords (one scale group per k-slice)
+        u32x4 wq[CT];
+#pragma unroll
+        for (int t = 0; t < CT; ++t) wq[t] = mma_swap<FMT>(wb[t]);
+#pragma unroll
+        for (int g = 0; g < GPQ; ++g) {
+            // int4 x bf16: sum(x) of the group's k per batch row (exact)
+            floatx4 sxv[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                sxv[rt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (BIAS) {
+                    constexpr uint32_t ONE2 = 0x3F803F80u;             // bf16 (1, 1)
+#pragma unroll
+                    for (int e = 0; e < SPG; ++e)
+                        sxv[rt] = mfma16<T>(xb[rt][g * SPG + e], u32x4{ONE2, ONE2, ONE2, ONE2}, sxv[rt]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < CT; ++t) {
+                if (t > 0) __builtin_amdgcn_sched_barrier(0);
+                u32x4 u[SPG];
+#pragma unroll
+                for (int e = 0; e < SPG; ++e) u[e] = unpack_slice<FMT, T>(wq[t], g * SPG + e);
+                const float sc = fp16_bits_to_f((uint16_t)(g ? sb[t] >> 16 : sb[t] & 0xFFFFu));
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    floatx4 d = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int e = 0; e < SPG; ++e) d = mfma16<T>(xb[rt][g * SPG + e], u[e], d);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float dr = BIAS ? __builtin_fmaf(-136.0f, sxv[rt][r], d[r]) : d[r];
+                        acc[rt][t][r] = __builtin_fmaf(sc, dr, acc[rt][t][r]);
+                    }
+                }
+            }
+        }
+    };
+
+    // the epilogue's inputs, behind the weights (used after the sums)
+    const uint32_t NT = blockDim.x;
+    constexpr uint32_t NO = RT * CT * 256;                     // output elements of the block
+    constexpr int EPT = (NO + 64 * 4 - 1) / (64 * 4);          // per thread, for KS >= 4
+    typename Epi::Pre pre[EPT];
+    auto out_mn = [&](uint32_t o, uint32_t& m, uint32_t& n) {
+        const uint32_t rt = o / (CT * 256), t = (o / 256) % CT, l = (o % 256) / 4, e = o % 4;
+        m = 16 * rt + 4 * (l / 16) + e;
+        n = 16 * (tile0 + t) + l % 16;
+    };
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        uint32_t m, n;
+        out_mn(min(threadIdx.x + NT * k, NO - 1), m, n);
+        pre[k] = epi.prefetch((int)min(m, M - 1), min(n, N - 1));
+    }
+#pragma unroll
+    for (int qd = 0; qd < QPW; ++qd) {
+        compute_q(wr[qd], sr[qd], xr[qd & 1]);
+        if (qd + 2 < QPW) load_x(qd + 2, xr[qd & 1]);
+    }
+
+    // ---- the KS partial sums of each output element, in wave order ----
+    floatx4* red = reinterpret_cast<floatx4*>(mm_lds);          // [wave][row tile][tile][lane]
+    const float* redf = reinterpret_cast<const float*>(mm_lds);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int t = 0; t < CT; ++t) red[((w * RT + rt) * CT + t) * WAVE + lane] = acc[rt][t];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        const uint32_t o = threadIdx.x + NT * k;
+        if (o < NO) {
+            float v = 0.0f;
+            for (uint32_t ww = 0; ww < KS; ++ww) v += redf[ww * NO + o];
+            uint32_t m, n;
+            out_mn(o, m, n);
+            if (m < M && n < N && o / 256 % CT + tile0 < tiles) epi((int)m, n, v, pre[k]);
+        }
+    }
+}
+
+// LSSM_MMA_STAGED=1 (read once) keeps packed x on the staging kernel, for A/B
+// measurements.
+inline bool mmx_disabled() {
+    static const bool off = [] {
+        const char* v = getenv("LSSM_MMA_STAGED");
+        return v && v[0] == '1';
+    }();
+    return off;
+}
+
+// ---- gemv_mmx launch plan: int4 group 64 x bf16; K split into KS (4..8)
+// waves of QPW (4, 5 or 8) quads; tiles per block from {1, 2, 3} so the
+// blocks cover the CUs about once ----
+struct MmxPlan {
+    uint32_t ct = 0, rt = 0, ks = 0, qpw = 0;
+    size_t lds = 0;
+};
+
+template <int FMT, typename T> bool mmx_plan(uint32_t M, uint32_t N, uint32_t K, MmxPlan& p) {
+    using P = Mma<FMT, T>;
+    if constexpr (FMT != LSSM_W_Q4_G64 || !__is_same(T, bf16)) {
+        return false;
+    } else {
+        if (M < 2 || M > 32 || N == 0 || K % P::QK != 0) return false;
+        const uint32_t quads = K / P::QK;
+        uint32_t ks = 0, qpw = 0;
+        for (uint32_t q : {4u, 5u, 8u})
+            if (ks == 0 && quads % q == 0 && quads / q >= 4 && quads / q <= (uint32_t)MMX_MAXW) {
+                qpw = q;
+                ks = quads / q;
+            }
+        if (ks == 0) return false;
+        const uint32_t tiles = (N + 15) / 16, cus = num_cus();
+        const uint32_t want = (tiles + cus - 1) / cus;
+        p.ct = want <= 1 ? 1 : (want == 2 ? 2 : 3);
+        p.rt = M > 16 ? 2 : 1;
+        p.ks = ks;
+        p.qpw = qpw;
+        p.lds = (size_t)ks * p.rt * p.ct * WAVE * 16;
+        return p.lds <= MM_LDS_MAX;
+    }
+}
+
+template <int FMT, typename T, int CT, int RT, int QPW, class Epi>
+hipError_t mmx_run(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmxPlan& p) {
+    auto k = gemv_mmx_kernel<FMT, T, CT, RT, QPW, Epi>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)MM_LDS_MAX);
+    if (attr != hipSuccess) return attr;
+    const uint32_t tiles = (c.N + 15) / 16;
+    k<<<(tiles + CT - 1) / CT, WAVE * p.ks, p.lds, s>>>(c, e, M);
+    return hipGetLastError();
+}
+
+template <int FMT, typename T, int CT, int RT, class Epi>
+hipError_t mmx_q(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmxPlan& p) {
+    switch (p.qpw) {
+        case 4: return mmx_run<FMT, T, CT, RT, 4, Epi>(s, c, e, M, p);
+        case 5: return mmx_run<FMT, T, CT, RT, 5, Epi>(s, c, e, M, p);
+        default: return mmx_run<FMT, T, CT, RT, 8, Epi>(s, c, e, M, p);
+    }
+}
+
+template <int FMT, typename T, class Epi>
+hipError_t mmx_go(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmxPlan& p) {
+    if constexpr (FMT == LSSM_W_Q4_G64 && __is_same(T, bf16)) {
+        if (p.rt == 1) {
+            switch (p.ct) {
+                case 1: return mmx_q<FMT, T, 1, 1, Epi>(s, c, e, M, p);
+                case 2: return mmx_q<FMT, T, 2, 1, Epi>(s, c, e, M, p);
+                default: return mmx_q<FMT, T, 3, 1, Epi>(s, c, e, M, p);
+            }
+        }
+        switch (p.ct) {
+            case 1: return mmx_q<FMT, T, 1, 2, Epi>(s, c, e, M, p);
+            case 2: return mmx_q<FMT, T, 2, 2, Epi>(s, c, e, M, p);
+            default: return mmx_q<FMT, T, 3, 2, Epi>(s, c, e, M, p);
+        }
+    } else {
+        return hipErrorInvalidValue;
+    }
+}
+
 // ---- gemv_mma launch plan ----
 struct MmaPlan {
     uint32_t ct = 0, qpw = 0, ks = 0, mpb = 0, ra = 0;
@@ -623,6 +865,12 @@ bool try_mma(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, int wfm
         constexpr int FMT = decltype(tag)::value;
         MmaPlan p;
         if (!mma_plan<FMT, T>(M, c.N, c.K, p)) return false;
+        // packed x of up to 32 rows: one pass without staging
+        MmxPlan q;
+        if (c.xp && !mmx_disabled() && mmx_plan<FMT, T>(M, c.N, c.K, q)) {
+            err = mmx_go<FMT, T, Epi>(s, c, e, M, q);
+            return true;
+        }
         err = c.xp ? mma_shape<FMT, T, true, true, Epi>(s, c, e, M, p)
                    : mma_shape<FMT, T, true, false, Epi>(s, c, e, M, p);
         return true;

@@ -131,14 +131,17 @@ PACK_CASES = [("f16-q8g32", O.F16, O.W_Q8_G32), ("f16-q4b32", O.F16, O.W_Q4_B32)
               ("bf16-q4g64", O.BF16, O.W_Q4_G64), ("f16-dense", O.F16, O.W_DENSE)]
 
 
+@pytest.mark.parametrize("B", [8, 24, 32])
 @pytest.mark.parametrize("tag,act,wfmt", PACK_CASES, ids=[c[0] for c in PACK_CASES])
-def test_engine_batch8_packed_staging(ctx, tag, act, wfmt):
-    """Batch 8 decode takes the packing pass (x normalised and packed once per
-    linear, then copied by every GEMV workgroup) for every format the MFMA
-    GEMV takes; against the oracle's per-sequence decode."""
+def test_engine_batch8_packed_staging(ctx, tag, act, wfmt, B):
+    """Decode batches from 8 rows take the packing pass (x normalised and
+    packed once per linear) and the single-pass MFMA GEMV, which reads the
+    packed rows straight from memory: 8 and 24/32 rows (one and two tiles of
+    16 batch rows), for every format the MFMA GEMV takes; against the
+    oracle's per-sequence decode."""
     from lite_ssm_amd.model import Engine
+    print(f"case: packed decode {tag} batch {B}", flush=True)
     L, sh, m, om = _setup(ctx, "mamba2-130m", act, wfmt, n_layer=2, vocab_size=1024, seed=17)
-    B = 8
     eng = Engine(ctx, m, max_batch=B, max_seq=40)
     try:
         ids = np.random.default_rng(3).integers(0, sh.vocab_size, (B, 40)).astype(np.int32)
@@ -150,7 +153,7 @@ def test_engine_batch8_packed_staging(ctx, tag, act, wfmt):
         for step in range(3):
             eng.decode(torch.from_numpy(tok).cuda(), nxt)
             ref = om.decode(conv, ssd, tok)
-            _check_logits(eng.logits(B).float().cpu().numpy(), ref, act, f"{tag} b8 decode {step}")
+            _check_logits(eng.logits(B).float().cpu().numpy(), ref, act, f"{tag} b{B} decode {step}")
             tok = O.argmax(ref, act)
     finally:
         eng.close()
