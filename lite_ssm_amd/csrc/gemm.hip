@@ -776,23 +776,56 @@ hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
         const size_t rw = (mt * (size_t)((a.N + 255) / 256) + cus - 1) / cus;
         const size_t rn = (mt * (size_t)((a.N + 127) / 128) + cus - 1) / cus;
         const bool wide = FMT != LSSM_W_DENSE && 3 * rw <= 2 * rn;
-        if (wide) {
-            dim3 grid((a.N + 255) / 256, mt);
+        auto run_wide = [&](const GemmArgs& g) {
+            dim3 grid((g.N + 255) / 256, mt);
             if constexpr (FMT != LSSM_W_DENSE) {
-                switch (a.epi) {
-                    case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU, 8><<<grid, 768, 0, s>>>(a); break;
-                    case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD, 8><<<grid, 768, 0, s>>>(a); break;
-                    default: gemm2_kernel<FMT, T, LSSM_EPI_NONE, 8><<<grid, 768, 0, s>>>(a); break;
+                switch (g.epi) {
+                    case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU, 8><<<grid, 768, 0, s>>>(g); break;
+                    case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD, 8><<<grid, 768, 0, s>>>(g); break;
+                    default: gemm2_kernel<FMT, T, LSSM_EPI_NONE, 8><<<grid, 768, 0, s>>>(g); break;
                 }
             }
+        };
+        auto run_narrow = [&](const GemmArgs& g) {
+            dim3 grid((g.N + 127) / 128, mt);
+            switch (g.epi) {
+                case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU, 4><<<grid, 512, 0, s>>>(g); break;
+                case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD, 4><<<grid, 512, 0, s>>>(g); break;
+                default: gemm2_kernel<FMT, T, LSSM_EPI_NONE, 4><<<grid, 512, 0, s>>>(g); break;
+            }
+        };
+        if (wide) {
+            // A last round of wide tiles at most half full (2.7B out_proj: 640
+            // tiles = 2.5 rounds) runs instead as one round of narrow tiles,
+            // which take about two thirds of a wide tile's time: the columns of
+            // the full rounds go to the wide launch, the rest to a narrow one
+            // (pointers offset by whole output columns, so each output is
+            // computed exactly as in the single launch).
+            const size_t wt = mt * (size_t)((a.N + 255) / 256);
+            const size_t full = wt / cus, rem = wt % cus;
+            const uint32_t n1 = full ? (uint32_t)((full * cus) / mt) * 256u : 0u;
+            const bool split = full >= 1 && rem > 0 && 2 * rem <= cus && n1 > 0 && n1 < a.N &&
+                               mt * (size_t)((a.N - n1 + 127) / 128) <= cus;
+            if (!split) {
+                run_wide(a);
+                return hipGetLastError();
+            }
+            GemmArgs a1 = a, a2 = a;
+            a1.N = n1;
+            a2.N = a.N - n1;
+            const size_t wrow = FMT == LSSM_W_Q8_G32 ? a.K : a.K / 2;     // packed bytes per W row
+            const uint32_t gs = FMT == LSSM_W_Q4_G64 ? 64u : 32u;
+            a2.w = (const uint8_t*)a.w + (size_t)n1 * wrow;
+            a2.s = (const uint16_t*)a.s + (size_t)n1 * (a.K / gs);
+            a2.y = (T*)a.y + n1;
+            if (a.res) a2.res = (const T*)a.res + n1;
+            run_wide(a1);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            run_narrow(a2);
             return hipGetLastError();
         }
-        dim3 grid((a.N + 127) / 128, mt);
-        switch (a.epi) {
-            case LSSM_EPI_SILU: gemm2_kernel<FMT, T, LSSM_EPI_SILU, 4><<<grid, 512, 0, s>>>(a); break;
-            case LSSM_EPI_ADD: gemm2_kernel<FMT, T, LSSM_EPI_ADD, 4><<<grid, 512, 0, s>>>(a); break;
-            default: gemm2_kernel<FMT, T, LSSM_EPI_NONE, 4><<<grid, 512, 0, s>>>(a); break;
-        }
+        run_narrow(a);
         return hipGetLastError();
     }
     dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);

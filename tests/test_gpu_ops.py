@@ -116,6 +116,24 @@ def test_gemm_wide_tiles(ctx, rng, wfmt):
     assert_close(act_host(y, act), ref, act, 1.6e-2, "gemm")
 
 
+@pytest.mark.parametrize("wfmt", [O.W_Q4_G64, O.W_Q4_B32, O.W_Q8_G32])
+def test_gemm_wide_tiles_split_tail(ctx, rng, wfmt):
+    """286 wide tiles on 256 CUs (a last round of 30): the columns of the full
+    round go to the wide launch and the remaining 336 (two and a partial
+    128-wide tile) to a narrow one, in place with the residual epilogue as the
+    engine's out_proj runs it."""
+    L = _lib()
+    act, M, N, K = O.BF16, 26 * 256, 2640, 192
+    print(f"case: split-tail GEMM {wfmt} M {M} N {N} K {K}", flush=True)
+    x = O.to_act(rng.standard_normal((M, K)), act)
+    w, s = _weights(rng, N, K, wfmt, act)
+    res = O.to_act(rng.standard_normal((M, N)), act)
+    yd = dev(res)
+    ctx.linear(dev(x), dev(w), dev(s), yd, M, N, K, wfmt, act, epi=L.EPI_ADD, residual=yd)
+    ref = O.linear(x, w, s, M, N, K, wfmt, act, epi=O.EPI_ADD, residual=res, round_dequant=1)
+    assert_close(act_host(yd, act), ref, act, 1.6e-2, "gemm split tail")
+
+
 @pytest.mark.parametrize("wfmt", [O.W_Q4_G64, O.W_Q8_G32, O.W_DENSE])
 @pytest.mark.parametrize("K", [64, 192])
 def test_gemm_one_and_odd_k_steps(ctx, rng, wfmt, K):
