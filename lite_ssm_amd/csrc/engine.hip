@@ -180,6 +180,9 @@ struct lssm_engine {
         const bool pack_in = B >= PACK_MIN_ROWS && d_model % 128 == 0 && gemv_mma_takes(B, proj, d_model, wfmt, act);
         const bool pack_out = B >= PACK_MIN_ROWS && d_inner % 128 == 0 &&
                               gemv_mma_takes(B, d_model, d_inner, wfmt, act);
+        // packed in the single-pass kernel's fragment order when it takes the call
+        const bool frag_in = pack_in && gemv_mmx_takes(B, proj, d_model, wfmt, act);
+        const bool frag_out = pack_out && gemv_mmx_takes(B, d_model, d_inner, wfmt, act);
         fused_layers = 0;
         mixer_layers = 0;
         if (e == hipSuccess) e = trace_rows(0, d_hidden, B);
@@ -218,7 +221,8 @@ struct lssm_engine {
                     mixer_layers += out_done ? 1u : 0u;
                 }
                 if (!ssd_done && pack_in) {
-                    e = launch_mma_pack(st(), d_hidden, d_model, w.norm_w, RMS_EPS, B, d_model, wfmt, act, d_gn);
+                    e = launch_mma_pack(st(), d_hidden, d_model, w.norm_w, RMS_EPS, B, d_model, wfmt, act, d_gn,
+                                        frag_in);
                     a.g.xpack = d_gn;
                 }
                 if (!ssd_done && e == hipSuccess) e = launch_inproj_decode(st(), a);
@@ -249,7 +253,8 @@ struct lssm_engine {
                 GemvArgs g{d_g, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden,
                            w.mixer_norm_w, RMS_EPS, B, d_model, d_inner, wfmt, act, LSSM_EPI_ADD};
                 if (pack_out) {
-                    e = launch_mma_pack(st(), d_g, d_inner, w.mixer_norm_w, RMS_EPS, B, d_inner, wfmt, act, d_gn);
+                    e = launch_mma_pack(st(), d_g, d_inner, w.mixer_norm_w, RMS_EPS, B, d_inner, wfmt, act, d_gn,
+                                        frag_out);
                     g.xpack = d_gn;
                 }
                 if (e == hipSuccess) e = launch_gemv(st(), g);
@@ -475,7 +480,8 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A(&e->d_xbc, (size_t)max_batch * e->xbc * es);
     A(&e->d_dt, (size_t)max_batch * e->H * es);
     A(&e->d_g, (size_t)max_batch * d_inner * es);
-    A(&e->d_gn, (size_t)max_batch * d_inner * es);
+    // (also the packed x rows of the MFMA decode GEMV: up to the next multiple of 16 rows)
+    A(&e->d_gn, (size_t)(max_batch + 15) / 16 * 16 * d_inner * es);
     A(&e->logits, (size_t)max_batch * e->vocab * es);
     A(&e->conv_state, (size_t)cfg->n_layer * max_batch * e->xbc * e->K * es);
     A((void**)&e->ssd_state, (size_t)cfg->n_layer * max_batch * e->H * e->P * e->N * sizeof(float));

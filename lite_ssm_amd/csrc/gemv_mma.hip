@@ -512,11 +512,13 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
 // gemv_mmx: the gemv_mma product for x packed by launch_mma_pack, 2..32 rows
 // in one pass (RT = 1 or 2 tiles of 16 batch rows), int4 group 64 x bf16
 // (the 2.7B / 8B decode linears).  Nothing is staged: the A fragments are
-// read straight from the packed rows (at most 32 rows of K / 2 dwords, which
-// stay in L2), and every unpacked weight slice meets all RT row tiles.  A
-// wave requests the x of its first two quads, then all its weights and
-// scales (one round trip to HBM per block), then, while it works through the
-// quads, the x of the quad two ahead.  (A wave's loads complete in the order
+// read straight from x packed in fragment order (launch_mma_pack, frag: at
+// most 32 rows, which stay in L2; each load instruction reads 1 KiB of
+// consecutive bytes, where the row-major rows would cost the vector L1 one
+// access per lane), and every unpacked weight slice meets all RT row tiles.  A
+// wave requests the x of its first XD quads (2 to 8, as registers allow),
+// then all its weights and scales (one round trip to HBM per block), then,
+// while it works through the quads, the x of the quad XD ahead.  (A wave's loads complete in the order
 // they were issued: x requested behind the weights could not be used before
 // every weight had arrived.)  The LDS holds only the KS partial sums, and a
 // block owns up to three tiles of 16 W rows so that the grid is about one
@@ -531,12 +533,12 @@ template <int FMT, typename T, int CT, int RT, int QPW, class Epi>
 __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi epi, uint32_t M) {
     using P = Mma<FMT, T>;
     using F = Fmt<FMT, T>;
-    constexpr int NP = P::NP, GPQ = P::GPQ, SPG = P::SPG, SPQ = P::SPQ;
+    constexpr int GPQ = P::GPQ, SPG = P::SPG, SPQ = P::SPQ;
     constexpr bool BIAS = P::BIAS;
     static_assert(P::G > 0 && GPQ == 2, "int4 group 64");
     extern __shared__ __attribute__((aligned(16))) uint32_t mm_lds[];
 
-    const uint32_t K = c.K, N = c.N, KH = K / 2;
+    const uint32_t K = c.K, N = c.N;
     const int lane = threadIdx.x % WAVE, li = lane % 16, lq = lane / 16;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     const uint32_t KS = blockDim.x / WAVE;
@@ -545,23 +547,25 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
     const size_t rb = F::row_bytes(K);
     epi.pin();
 
-    const uint32_t* xrow[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) xrow[rt] = c.xp + (size_t)min(16u * rt + li, M - 1) * KH;
-    u32x4 xr[2][RT][SPQ];                                      // x of two quads
+    // x in fragment order (launch_mma_pack, frag): the 16 bytes lane l supplies
+    // to k-slice s of quad qa for row tile rt at u32x4 ((rt quads + qa) SPQ + s) 64 + l,
+    // so each of these loads reads 1 KiB of consecutive bytes
+    const u32x4* xf = reinterpret_cast<const u32x4*>(c.xp);
+    const uint32_t quads = K / P::QK;
+    // x of XD quads in flight (a ring): as many as the registers left by the
+    // weights and sums allow, at least two
+    constexpr int XD = CT == 1 ? (QPW < (RT == 2 ? 4 : 8) ? QPW : (RT == 2 ? 4 : 8))
+                               : (CT == 2 ? (QPW < 3 ? QPW : 3) : (QPW < 2 ? QPW : 2));
+    u32x4 xr[XD][RT][SPQ];
     auto load_x = [&](int qd, u32x4 (&xb)[RT][SPQ]) {
         const uint32_t qa = qa0 + qd;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int sl = 0; sl < SPQ; ++sl) {
-                int ch, po;
-                mma_slice_pos<FMT>(sl, lq, ch, po);
-                xb[rt][sl] = *reinterpret_cast<const u32x4*>(xrow[rt] + (4 * qa + ch) * NP + po);
-            }
+            for (int sl = 0; sl < SPQ; ++sl) xb[rt][sl] = xf[(((size_t)rt * quads + qa) * SPQ + sl) * WAVE + lane];
     };
-    load_x(0, xr[0]);
-    if (QPW > 1) load_x(1, xr[1]);
+#pragma unroll
+    for (int qd = 0; qd < XD; ++qd) load_x(qd, xr[qd]);
     // all weights and scales of the wave's quads
     u32x4 wr[QPW][CT];
     uint32_t sr[QPW][CT];                                      // the quad's two group scales
@@ -641,8 +645,8 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
     }
 #pragma unroll
     for (int qd = 0; qd < QPW; ++qd) {
-        compute_q(wr[qd], sr[qd], xr[qd & 1]);
-        if (qd + 2 < QPW) load_x(qd + 2, xr[qd & 1]);
+        compute_q(wr[qd], sr[qd], xr[qd % XD]);
+        if (qd + XD < QPW) load_x(qd + XD, xr[qd % XD]);
     }
 
     // ---- the KS partial sums of each output element, in wave order ----
@@ -887,16 +891,21 @@ template <typename T> bool mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfm
 // ---- x normalised and packed once for a whole gemv_mma launch ----
 // Row m: rr = 1 / sqrt(mean(x^2) + eps), then each octet's r(x w rr) in the
 // staging's pair order (norm.metal:52-79), stored as the staging would put it
-// in LDS (pairs of k .. k + 7 at dwords k / 2 .. k / 2 + 3 of the row).
-template <int FMT, typename T>
+// in LDS (pairs of k .. k + 7 at dwords k / 2 .. k / 2 + 3 of the row) or, with
+// FRAG (int4 group 64 only), in gemv_mmx_kernel's fragment order: the 16 bytes
+// lane l = 16 q + (m % 16) supplies to k-slice s of quad qa for row tile m / 16
+// at u32x4 ((m / 16 quads + qa) 4 + s) 64 + l.  With FRAG the grid covers the
+// rows up to the next multiple of 16, and rows past M are zeros.
+template <int FMT, typename T, bool FRAG>
 __global__ __launch_bounds__(1024) void mma_pack_kernel(const T* x, uint32_t x_stride, const T* nw, float eps,
-                                                        uint32_t K, uint32_t* out) {
+                                                        uint32_t K, uint32_t M, uint32_t* out) {
     // one octet per thread (blockDim.x >= K / 8), x and w read once
     __shared__ float red[1024 / WAVE];
     const uint32_t m = blockIdx.x, KO = K / 8, cc = threadIdx.x;
     const bool live = cc < KO;
+    const bool row = !FRAG || m < M;
     u32x4 xv = u32x4{0u, 0u, 0u, 0u}, nv = xv;
-    if (live) {
+    if (live && row) {
         xv = reinterpret_cast<const u32x4*>(x + (size_t)m * x_stride)[cc];
         nv = reinterpret_cast<const u32x4*>(nw)[cc];
     }
@@ -926,25 +935,41 @@ __global__ __launch_bounds__(1024) void mma_pack_kernel(const T* x, uint32_t x_s
         octet_pos<FMT, T>(qq, pa, pb);
         pk[qq] = pack2<T>(v[pa], v[pb]);
     }
-    reinterpret_cast<u32x4*>(out + (size_t)m * (K / 2))[cc] = pk;
+    if constexpr (FRAG) {
+        // octet cc = 16 qa + 4 ch + p (chunk ch, pair offset 4 p of the quad):
+        // k-slice s and lane group q with mma_slice_pos(s, q) = (ch, 4 p)
+        const uint32_t qa = cc / 16, ch = (cc % 16) / 4, p4 = cc % 4;
+        const uint32_t sl = 2 * (ch >> 1) + (p4 & 1), lg = (ch & 1) + 2 * (p4 >> 1);
+        const uint32_t quads = K / 128;
+        reinterpret_cast<u32x4*>(out)[(((size_t)(m / 16) * quads + qa) * 4 + sl) * WAVE + 16 * lg + m % 16] = pk;
+    } else {
+        reinterpret_cast<u32x4*>(out + (size_t)m * (K / 2))[cc] = pk;
+    }
 }
 
 }  // namespace
 
 hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, const void* norm_w, float eps,
-                           uint32_t M, uint32_t K, int wfmt, int act, void* out) {
+                           uint32_t M, uint32_t K, int wfmt, int act, void* out, bool frag) {
     if (M == 0 || K % 128 != 0 || K > 8192 || (uintptr_t)x % 16 || (x_stride * 2u) % 16 ||
         (uintptr_t)norm_w % 16 || (uintptr_t)out % 16)
         return hipErrorInvalidValue;
+    if (frag && (wfmt != LSSM_W_Q4_G64 || act != LSSM_BF16)) return hipErrorInvalidValue;
     const uint32_t nt = (K / 8 + WAVE - 1) / WAVE * WAVE;      // one octet per thread
+    if (frag) {
+        mma_pack_kernel<LSSM_W_Q4_G64, bf16, true><<<(M + 15) / 16 * 16, nt, 0, s>>>(
+            static_cast<const bf16*>(x), x_stride, static_cast<const bf16*>(norm_w), eps, K, M,
+            static_cast<uint32_t*>(out));
+        return hipGetLastError();
+    }
     hipError_t err = hipErrorInvalidValue;
     auto go = [&](auto tag) -> bool {
         using T = decltype(tag);
         return mma_fmt<T>(wfmt, [&](auto ft) -> bool {
             constexpr int FMT = decltype(ft)::value;
-            mma_pack_kernel<FMT, T><<<M, nt, 0, s>>>(static_cast<const T*>(x), x_stride,
-                                                      static_cast<const T*>(norm_w), eps, K,
-                                                      static_cast<uint32_t*>(out));
+            mma_pack_kernel<FMT, T, false><<<M, nt, 0, s>>>(static_cast<const T*>(x), x_stride,
+                                                             static_cast<const T*>(norm_w), eps, K, M,
+                                                             static_cast<uint32_t*>(out));
             err = hipGetLastError();
             return true;
         });
@@ -952,6 +977,12 @@ hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, cons
     if (act == LSSM_F16) go(f16{});
     else if (act == LSSM_BF16) go(bf16{});
     return err;
+}
+
+bool gemv_mmx_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
+    if (act != LSSM_BF16 || wfmt != LSSM_W_Q4_G64 || mmx_disabled()) return false;
+    MmxPlan p;
+    return mmx_plan<LSSM_W_Q4_G64, bf16>(M, N, K, p);
 }
 
 bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {

@@ -270,6 +270,11 @@ bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);
 // decode GEMV's staging order for `wfmt`, into out ([M][K / 2] dwords): one
 // pass for all blocks of the GEMV launch that follows (GemvArgs::xpack).
 hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, const void* norm_w,
-                           float eps, uint32_t M, uint32_t K, int wfmt, int act, void* out);
+                           float eps, uint32_t M, uint32_t K, int wfmt, int act, void* out,
+                           bool frag = false);
+// The MFMA decode GEMV takes (M, N, K) in its single-pass form, which reads x
+// packed in fragment order (launch_mma_pack with frag = true; the buffer then
+// holds ceil(M / 16) * 16 rows).
+bool gemv_mmx_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);
 
 }  // namespace lssm
