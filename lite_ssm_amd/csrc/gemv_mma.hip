@@ -522,14 +522,21 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
 // they were issued: x requested behind the weights could not be used before
 // every weight had arrived.)  The LDS holds only the KS partial sums, and a
 // block owns up to three tiles of 16 W rows so that the grid is about one
-// block per CU.  Per wave, the k-slices and the group scaling are
+// block per CU; where three would leave more blocks than CUs (the 8B
+// in_proj: 1160 tiles), 8-wave blocks take four or five, keep one scale
+// register per tile and, by default, run their quads through a ring of two
+// (x and weights of two quads in flight).  Weights are read with ordinary
+// loads: a load instruction reads 64 bytes of each of 16 rows, the other half
+// of each 128-byte line is the next quad's, and nontemporal loads lost the
+// line in between (8B in_proj at batch 32: 51.5 MB fetched from HBM against
+// 44.5 MB, 19.4 against 16.1 us).  Per wave, the k-slices and the group scaling are
 // gemv_mma_kernel's and the partials are summed in wave order; the K split
 // (at most 8 waves here) can differ from that kernel's, so the two may round
 // the fp32 sum of an output differently.
 // ---------------------------------------------------------------------------
 constexpr int MMX_MAXW = 8;                      // waves per block: the K split
 
-template <int FMT, typename T, int CT, int RT, int QPW, class Epi>
+template <int FMT, typename T, int CT, int RT, int QPW, int DR, class Epi>
 __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi epi, uint32_t M) {
     using P = Mma<FMT, T>;
     using F = Fmt<FMT, T>;
@@ -564,21 +571,52 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
 #pragma unroll
             for (int sl = 0; sl < SPQ; ++sl) xb[rt][sl] = xf[(((size_t)rt * quads + qa) * SPQ + sl) * WAVE + lane];
     };
+    // DR > 0: x and weights of DR quads in flight (a ring of quads), so that
+    // the products of a quad overlap the loads of the ones after it
+    constexpr bool RING = DR > 0;
+    if constexpr (!RING) {
 #pragma unroll
-    for (int qd = 0; qd < XD; ++qd) load_x(qd, xr[qd]);
-    // all weights and scales of the wave's quads
+        for (int qd = 0; qd < XD; ++qd) load_x(qd, xr[qd]);
+    }
+    // all weights and scales of the wave's quads.  Blocks of more than three
+    // tiles (four quads a wave) keep one scale register per tile: lane group
+    // q holds its row's scales of quad q, handed to the other lanes as needed.
+    constexpr bool SQ = CT > 3;
+    static_assert(!SQ || QPW == 4, "one quad per lane group");
+    constexpr int SR = SQ ? 1 : QPW;
+    // Requested quad by quad (all tiles of a quad together), so that the
+    // first quads' products start while the later weights are on their way.
     u32x4 wr[QPW][CT];
-    uint32_t sr[QPW][CT];                                      // the quad's two group scales
+    uint32_t sr[SR][CT];                                       // the quad's two group scales
+    const uint8_t* wp[CT];
+    const uint32_t* sp[CT];
 #pragma unroll
     for (int t = 0; t < CT; ++t) {
         const uint32_t n = min(16 * (tile0 + t) + li, N - 1);
-        const uint8_t* wp = c.w + n * rb + 16 * lq;
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(c.s + (size_t)n * (K / P::G));
+        wp[t] = c.w + n * rb + 16 * lq + 64 * qa0;
+        sp[t] = reinterpret_cast<const uint32_t*>(c.s + (size_t)n * (K / P::G)) + qa0;
+        if constexpr (SQ) sr[0][t] = sp[t][lq];
+    }
+    static_assert(!RING || SQ, "the ring keeps the scales of all quads");
+    constexpr int NR = RING ? DR : 1;
+    u32x4 xg[NR][RT][SPQ], wg[NR][CT];
+    auto load_q = [&](int qd, int slot) {
+        load_x(qd, xg[slot]);
 #pragma unroll
-        for (int qd = 0; qd < QPW; ++qd) {
-            wr[qd][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp + 64 * (qa0 + qd)));
-            sr[qd][t] = sp[qa0 + qd];
-        }
+        for (int t = 0; t < CT; ++t)
+            wg[slot][t] = *reinterpret_cast<const u32x4*>(wp[t] + 64 * qd);
+    };
+    if constexpr (RING) {
+#pragma unroll
+        for (int qd = 0; qd < DR; ++qd) load_q(qd, qd);
+    } else {
+#pragma unroll
+        for (int qd = 0; qd < QPW; ++qd)
+#pragma unroll
+            for (int t = 0; t < CT; ++t) {
+                wr[qd][t] = *reinterpret_cast<const u32x4*>(wp[t] + 64 * qd);
+                if constexpr (!SQ) sr[qd][t] = sp[t][qd];
+            }
     }
 
     floatx4 acc[RT][CT];
@@ -630,24 +668,44 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
     // the epilogue's inputs, behind the weights (used after the sums)
     const uint32_t NT = blockDim.x;
     constexpr uint32_t NO = RT * CT * 256;                     // output elements of the block
-    constexpr int EPT = (NO + 64 * 4 - 1) / (64 * 4);          // per thread, for KS >= 4
+    constexpr uint32_t NTMIN = CT > 3 ? 64 * 8 : 64 * 4;       // blocks of > 3 tiles have 8 waves
+    constexpr int EPT = (NO + NTMIN - 1) / NTMIN;              // per thread
     typename Epi::Pre pre[EPT];
     auto out_mn = [&](uint32_t o, uint32_t& m, uint32_t& n) {
         const uint32_t rt = o / (CT * 256), t = (o / 256) % CT, l = (o % 256) / 4, e = o % 4;
         m = 16 * rt + 4 * (l / 16) + e;
         n = 16 * (tile0 + t) + l % 16;
     };
+    auto prefetch = [&] {
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        uint32_t m, n;
-        out_mn(min(threadIdx.x + NT * k, NO - 1), m, n);
-        pre[k] = epi.prefetch((int)min(m, M - 1), min(n, N - 1));
-    }
+        for (int k = 0; k < EPT; ++k) {
+            uint32_t m, n;
+            out_mn(min(threadIdx.x + NT * k, NO - 1), m, n);
+            pre[k] = epi.prefetch((int)min(m, M - 1), min(n, N - 1));
+        }
+    };
+    // (blocks of more than three tiles have no registers to spare for them
+    // during the sums: their epilogue inputs are requested behind the last quad)
+    if constexpr (!SQ) prefetch();
 #pragma unroll
     for (int qd = 0; qd < QPW; ++qd) {
-        compute_q(wr[qd], sr[qd], xr[qd % XD]);
+        if constexpr (SQ) {
+            uint32_t sb[CT];
+#pragma unroll
+            for (int t = 0; t < CT; ++t) sb[t] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (16 * qd + li), (int)sr[0][t]);
+            if constexpr (RING) {
+                compute_q(wg[qd % DR], sb, xg[qd % DR]);
+                if (qd + DR < QPW) load_q(qd + DR, qd % DR);
+                continue;
+            }
+            compute_q(wr[qd], sb, xr[qd % XD]);
+        } else {
+            compute_q(wr[qd], sr[qd], xr[qd % XD]);
+        }
         if (qd + XD < QPW) load_x(qd + XD, xr[qd % XD]);
     }
+
+    if constexpr (SQ) prefetch();
 
     // ---- the KS partial sums of each output element, in wave order ----
     floatx4* red = reinterpret_cast<floatx4*>(mm_lds);          // [wave][row tile][tile][lane]
@@ -680,6 +738,14 @@ inline bool mmx_disabled() {
     return off;
 }
 
+inline bool mmx_wide() {
+    static const bool on = [] {
+        const char* v = getenv("LSSM_MMX_WIDE");
+        return !v || v[0] != '0';
+    }();
+    return on;
+}
+
 // ---- gemv_mmx launch plan: int4 group 64 x bf16; K split into KS (4..8)
 // waves of QPW (4, 5 or 8) quads; tiles per block from {1, 2, 3} so the
 // blocks cover the CUs about once ----
@@ -705,6 +771,8 @@ template <int FMT, typename T> bool mmx_plan(uint32_t M, uint32_t N, uint32_t K,
         const uint32_t tiles = (N + 15) / 16, cus = num_cus();
         const uint32_t want = (tiles + cus - 1) / cus;
         p.ct = want <= 1 ? 1 : (want == 2 ? 2 : 3);
+        // 4 or 5 tiles (the 8B in_proj): built for 8 waves of 4 quads
+        if (want > 3 && qpw == 4 && ks == (uint32_t)MMX_MAXW && mmx_wide()) p.ct = want > 5 ? 5 : want;
         p.rt = M > 16 ? 2 : 1;
         p.ks = ks;
         p.qpw = qpw;
@@ -713,9 +781,9 @@ template <int FMT, typename T> bool mmx_plan(uint32_t M, uint32_t N, uint32_t K,
     }
 }
 
-template <int FMT, typename T, int CT, int RT, int QPW, class Epi>
+template <int FMT, typename T, int CT, int RT, int QPW, class Epi, int DR = 0>
 hipError_t mmx_run(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmxPlan& p) {
-    auto k = gemv_mmx_kernel<FMT, T, CT, RT, QPW, Epi>;
+    auto k = gemv_mmx_kernel<FMT, T, CT, RT, QPW, DR, Epi>;
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)MM_LDS_MAX);
     if (attr != hipSuccess) return attr;
@@ -733,6 +801,23 @@ hipError_t mmx_q(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, con
     }
 }
 
+// blocks of 4 or 5 tiles: quads in a ring of mmx_ring() (0: all weights up front)
+inline int mmx_ring() {
+    static const int r = [] {
+        const char* v = getenv("LSSM_MMX_RING");
+        return v ? (int)strtol(v, nullptr, 10) : 2;
+    }();
+    return r;
+}
+
+template <int FMT, typename T, int CT, int RT, class Epi>
+hipError_t mmx_wide(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmxPlan& p) {
+    switch (mmx_ring()) {
+        case 0: return mmx_run<FMT, T, CT, RT, 4, Epi, 0>(s, c, e, M, p);
+        default: return mmx_run<FMT, T, CT, RT, 4, Epi, 2>(s, c, e, M, p);
+    }
+}
+
 template <int FMT, typename T, class Epi>
 hipError_t mmx_go(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmxPlan& p) {
     if constexpr (FMT == LSSM_W_Q4_G64 && __is_same(T, bf16)) {
@@ -740,13 +825,17 @@ hipError_t mmx_go(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, co
             switch (p.ct) {
                 case 1: return mmx_q<FMT, T, 1, 1, Epi>(s, c, e, M, p);
                 case 2: return mmx_q<FMT, T, 2, 1, Epi>(s, c, e, M, p);
-                default: return mmx_q<FMT, T, 3, 1, Epi>(s, c, e, M, p);
+                case 3: return mmx_q<FMT, T, 3, 1, Epi>(s, c, e, M, p);
+                case 4: return mmx_wide<FMT, T, 4, 1, Epi>(s, c, e, M, p);
+                default: return mmx_wide<FMT, T, 5, 1, Epi>(s, c, e, M, p);
             }
         }
         switch (p.ct) {
             case 1: return mmx_q<FMT, T, 1, 2, Epi>(s, c, e, M, p);
             case 2: return mmx_q<FMT, T, 2, 2, Epi>(s, c, e, M, p);
-            default: return mmx_q<FMT, T, 3, 2, Epi>(s, c, e, M, p);
+            case 3: return mmx_q<FMT, T, 3, 2, Epi>(s, c, e, M, p);
+            case 4: return mmx_wide<FMT, T, 4, 2, Epi>(s, c, e, M, p);
+            default: return mmx_wide<FMT, T, 5, 2, Epi>(s, c, e, M, p);
         }
     } else {
         return hipErrorInvalidValue;
@@ -862,9 +951,21 @@ template <typename T, class F> bool mma_fmt(int wfmt, F&& f) {
 // Runs the MFMA decode kernel when it takes this call (returns false, and
 // launches nothing, otherwise).
 // Only RMSNorm-fused calls (the engine's decode linears and inproj_decode).
+// Batches below this many rows go to the VALU GEMV (gemv1 takes up to 4):
+// at 2 rows it is the faster of the two (2.7B decode at batch 2: 1470 against
+// 1406 tok/s), at 3 and 4 the MFMA kernel (1953 / 2453 against 1170 / 1492).
+// LSSM_MMA_MIN_ROWS=n overrides it, for A/B measurements.
+inline uint32_t mma_min_rows() {
+    static const uint32_t r = [] {
+        const char* v = getenv("LSSM_MMA_MIN_ROWS");
+        return v ? (uint32_t)strtoul(v, nullptr, 10) : 3u;
+    }();
+    return r;
+}
+
 template <typename T, class Epi>
 bool try_mma(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, int wfmt, bool norm, hipError_t& err) {
-    if (!norm || !mma_aligned<T>(c, norm)) return false;
+    if (!norm || M < mma_min_rows() || !mma_aligned<T>(c, norm)) return false;
     return mma_fmt<T>(wfmt, [&](auto tag) -> bool {
         constexpr int FMT = decltype(tag)::value;
         MmaPlan p;
@@ -882,6 +983,7 @@ bool try_mma(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, int wfm
 }
 
 template <typename T> bool mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt) {
+    if (M < mma_min_rows()) return false;
     return mma_fmt<T>(wfmt, [&](auto tag) -> bool {
         MmaPlan p;
         return mma_plan<decltype(tag)::value, T>(M, N, K, p);

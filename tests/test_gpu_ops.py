@@ -40,7 +40,7 @@ def test_dequant_bit_exact(ctx, rng, wfmt):
 # --------------------------------------------------------------------------- GEMV / GEMM
 @pytest.mark.parametrize("act", ACTS)
 @pytest.mark.parametrize("wfmt", ALL_FMTS)
-@pytest.mark.parametrize("M", [1, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_gemv_vs_oracle(ctx, rng, act, wfmt, M):
     L = _lib()
     N, K = 200, 768
