@@ -517,8 +517,8 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
     // The small loads (a 2-byte scale per chunk, the epilogue's inputs) go out
     // here, while the memory system is quiet: issued behind the weights they
     // would hold the wave as long as the weight traffic pushes back.  The
-    // 16-byte weight chunks are requested after the last barrier.  Scheduling
-    // barriers pin the issue order; waits count loads in issue order.
+    // 16-byte weight chunks follow (below).  Scheduling barriers pin the issue
+    // order; waits count loads in issue order.
     const uint32_t nwaves = gridDim.x * NWB;
     const uint32_t wv = blockIdx.x * NWB + threadIdx.x / WAVE;
     auto load_side = [&](RowSet<CPL, MR, Epi>& rs, uint32_t group) {
@@ -546,12 +546,17 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
     };
     RowSet<CPL, MR, Epi> A;
     load_side(A, wv);
+    // With the RMSNorm prologue (the decode linears) the weights are requested
+    // right behind x: x still returns first (a wave's loads return in issue
+    // order) and the weights stream in while x is normalised and staged
+    // (2.7B batch-1 decode: in_proj + SSD 9.36 -> 8.76 us, out_proj 5.32 ->
+    // 4.64 us, 1001 -> 1104 tok/s, against requesting them after the staging
+    // barrier; a barrier between the x and the weight requests cost 1 %).
+    constexpr bool EARLY_W = NORM && !LOOP;
+    if constexpr (EARLY_W) load_w(A);
 
-    // ---- 1b. sum(x^2) and 1/rms, finished before any weight is requested ----
-    // Requested together with the weights, x queues behind the whole chip's
-    // weight misses in L2 (~2.5 us); alone it returns in well under 1 us, and
-    // normalising and staging then overlap the weight stream.  sum(x^2) uses
-    // v_dot2 on packed pairs (exact products, fp32 sums).
+    // ---- 1b. sum(x^2) and 1/rms ----
+    // sum(x^2) uses v_dot2 on packed pairs (exact products, fp32 sums).
     float rr[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) rr[m] = 1.0f;
@@ -650,10 +655,8 @@ __global__ __launch_bounds__(NTMAX) void gemv1_kernel(GemvCore c, Epi epi, uint3
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Weights are requested after the last barrier: a wave issuing loads is
-    // held for as long as the memory system pushes back, and no barrier may
-    // wait on that.
-    load_w(A);
+    // Otherwise the weights are requested after the last barrier.
+    if constexpr (!EARLY_W) load_w(A);
     [[maybe_unused]] typename EarlyOf<Epi>::type early;
     if constexpr (Epi::kTail) epi.early(early);
 
