@@ -523,7 +523,7 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
 // every weight had arrived.)  The LDS holds only the KS partial sums, and a
 // block owns up to three tiles of 16 W rows so that the grid is about one
 // block per CU; where three would leave more blocks than CUs (the 8B
-// in_proj: 1160 tiles), 8-wave blocks take four or five, keep one scale
+// in_proj: 1160 tiles), 8-wave blocks take five, keep one scale
 // register per tile and, by default, run their quads through a ring of two
 // (x and weights of two quads in flight).  Weights are read with ordinary
 // loads: a load instruction reads 64 bytes of each of 16 rows, the other half
@@ -771,8 +771,8 @@ template <int FMT, typename T> bool mmx_plan(uint32_t M, uint32_t N, uint32_t K,
         const uint32_t tiles = (N + 15) / 16, cus = num_cus();
         const uint32_t want = (tiles + cus - 1) / cus;
         p.ct = want <= 1 ? 1 : (want == 2 ? 2 : 3);
-        // 4 or 5 tiles (the 8B in_proj): built for 8 waves of 4 quads
-        if (want > 3 && qpw == 4 && ks == (uint32_t)MMX_MAXW && mmx_wide()) p.ct = want > 5 ? 5 : want;
+        // 5 tiles (the 8B in_proj): built for 8 waves of 4 quads
+        if (want > 3 && qpw == 4 && ks == (uint32_t)MMX_MAXW && mmx_wide()) p.ct = 5;
         p.rt = M > 16 ? 2 : 1;
         p.ks = ks;
         p.qpw = qpw;
@@ -801,7 +801,7 @@ hipError_t mmx_q(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, con
     }
 }
 
-// blocks of 4 or 5 tiles: quads in a ring of mmx_ring() (0: all weights up front)
+// blocks of 5 tiles: quads in a ring of mmx_ring() (0: all weights up front)
 inline int mmx_ring() {
     static const int r = [] {
         const char* v = getenv("LSSM_MMX_RING");
@@ -826,7 +826,6 @@ hipError_t mmx_go(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, co
                 case 1: return mmx_q<FMT, T, 1, 1, Epi>(s, c, e, M, p);
                 case 2: return mmx_q<FMT, T, 2, 1, Epi>(s, c, e, M, p);
                 case 3: return mmx_q<FMT, T, 3, 1, Epi>(s, c, e, M, p);
-                case 4: return mmx_wide<FMT, T, 4, 1, Epi>(s, c, e, M, p);
                 default: return mmx_wide<FMT, T, 5, 1, Epi>(s, c, e, M, p);
             }
         }
@@ -834,7 +833,6 @@ hipError_t mmx_go(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, co
             case 1: return mmx_q<FMT, T, 1, 2, Epi>(s, c, e, M, p);
             case 2: return mmx_q<FMT, T, 2, 2, Epi>(s, c, e, M, p);
             case 3: return mmx_q<FMT, T, 3, 2, Epi>(s, c, e, M, p);
-            case 4: return mmx_wide<FMT, T, 4, 2, Epi>(s, c, e, M, p);
             default: return mmx_wide<FMT, T, 5, 2, Epi>(s, c, e, M, p);
         }
     } else {

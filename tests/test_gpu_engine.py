@@ -159,6 +159,33 @@ def test_engine_batch8_packed_staging(ctx, tag, act, wfmt, B):
         eng.close()
 
 
+@pytest.mark.parametrize("B", [8, 24])
+def test_engine_8b_widths_packed_decode(ctx, B):
+    """8B layer widths (d_model 4096, in_proj 18560 rows, G 8) at decode batches
+    8 and 24: the packing pass and the single-pass MFMA GEMV with five 16-row
+    tiles per block (in_proj) at one and two tiles of batch rows, and the
+    K 8192 out_proj; against the oracle's per-sequence decode."""
+    from lite_ssm_amd.model import Engine
+    print(f"case: 8B widths, packed decode batch {B}", flush=True)
+    L, sh, m, om = _setup(ctx, "mamba2-8b", O.BF16, O.W_Q4_G64, n_layer=1, vocab_size=512, seed=23)
+    Lq = 8
+    eng = Engine(ctx, m, max_batch=B, max_seq=Lq)
+    try:
+        ids = np.random.default_rng(5).integers(0, sh.vocab_size, (B, Lq)).astype(np.int32)
+        nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+        eng.prefill(torch.from_numpy(ids).cuda(), nxt)
+        conv, ssd = om.new_state(B)
+        ref = om.prefill(conv, ssd, ids)
+        tok = O.argmax(ref, O.BF16)
+        for step in range(2):
+            eng.decode(torch.from_numpy(tok).cuda(), nxt)
+            ref = om.decode(conv, ssd, tok)
+            _check_logits(eng.logits(B).float().cpu().numpy(), ref, O.BF16, f"8B widths b{B} decode {step}")
+            tok = O.argmax(ref, O.BF16)
+    finally:
+        eng.close()
+
+
 def test_engine_one_token_prefill(ctx):
     """L == 1 prefill takes the reference's GEMV / conv-update / SSD-step path
     and seeds the conv state (mamba2_block.cpp:111-116, 155-162, 183-195, 285-289)."""
