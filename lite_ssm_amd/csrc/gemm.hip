@@ -536,6 +536,74 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
     // row (r/4)*8 + (l/32)*4 + r%4, column l%32.
     T* Y = (T*)a.y;
     const T* Rz = (const T*)a.res;
+    const bool vec = a.y_stride % 8 == 0 && (uintptr_t)a.y % 16 == 0 &&
+                     (EPI != LSSM_EPI_ADD || (uintptr_t)a.res % 16 == 0);
+    if (vec) {
+        // The tile goes through LDS (rows 0..127 over the X stages, 128..255
+        // over the W stages) as the rounded outputs, then out in 16-byte runs
+        // of 8 columns: scattered 2-byte stores (and residual loads) cost the
+        // tile's last round ~13 % of the out_proj launch.  Same arithmetic:
+        // r(acc) / r(silu(acc)) staged, the residual added to the staged value.
+        constexpr uint32_t RB = BN * 2;                        // staged row bytes
+        char* half = wm == 0 ? reinterpret_cast<char*>(&As[0][0]) : reinterpret_cast<char*>(&Bs[0][0]);
+        // 16-byte slot s of row r sits at slot s ^ 4 ((r / 4) % 2): rows r and
+        // r + 4 (one store instruction) fall in different banks
+        auto slot_of = [](uint32_t r, uint32_t sl) { return sl ^ (4u * ((r >> 2) & 1u)); };
+        barrier();                                             // every wave's DMAs and reads done
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t c = wn * 64 + j * 32 + lane % 32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t rr = i * 32 + (r / 4) * 8 + (lane / 32) * 4 + r % 4;
+                    float v = acc[i][j][r];
+                    if (EPI == LSSM_EPI_SILU) v = silu_f(v);
+                    *reinterpret_cast<T*>(half + rr * RB + 16 * slot_of(rr, c / 8) + 2 * (c % 8)) = from_f<T>(v);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);                    // lgkmcnt(0)
+        barrier();
+        constexpr uint32_t SPR = BN / 8;                       // slots per row
+        constexpr uint32_t NT = 64 * CW;
+#pragma unroll 4
+        for (uint32_t q = threadIdx.x; q < G2M * SPR; q += NT) {
+            const uint32_t R = q / SPR, sl = q % SPR, rr = R % 128;
+            const char* hp = R < 128 ? reinterpret_cast<const char*>(&As[0][0]) : reinterpret_cast<const char*>(&Bs[0][0]);
+            const u32x4 st = *reinterpret_cast<const u32x4*>(hp + rr * RB + 16 * slot_of(rr, sl));
+            const uint32_t m = m0 + R, n = n0 + 8 * sl;
+            if (m >= a.M) continue;
+            const size_t yi = (size_t)m * a.y_stride + n;
+            if (n + 8 <= a.N) {
+                if constexpr (EPI == LSSM_EPI_ADD) {
+                    const u32x4 rv = *reinterpret_cast<const u32x4*>(Rz + yi);
+                    u32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float lo = f_of_bits<T>((uint16_t)rv[e]) + f_of_bits<T>((uint16_t)st[e]);
+                        const float hi = f_of_bits<T>((uint16_t)(rv[e] >> 16)) + f_of_bits<T>((uint16_t)(st[e] >> 16));
+                        o[e] = (uint32_t)__builtin_bit_cast(uint16_t, from_f<T>(lo)) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, from_f<T>(hi)) << 16);
+                    }
+                    *reinterpret_cast<u32x4*>(Y + yi) = o;
+                } else {
+                    *reinterpret_cast<u32x4*>(Y + yi) = st;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    if (n + e >= a.N) break;
+                    const uint16_t sb = (uint16_t)(st[e / 2] >> (16 * (e % 2)));
+                    float v = f_of_bits<T>(sb);
+                    if (EPI == LSSM_EPI_ADD) v = to_f(Rz[yi + e]) + v;
+                    Y[yi + e] = from_f<T>(v);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
