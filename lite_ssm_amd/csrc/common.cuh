@@ -92,6 +92,19 @@ template <int W> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Half-word index of element (m, k) of x in the single-pass MFMA decode
+// GEMV's fragment order (int4 group 64 x bf16; quads = K / 128): octet k / 8 =
+// 16 qa + 4 ch + p4 of row m is the 16 bytes lane 16 lg + m % 16 supplies to
+// k-slice sl = 2 (ch >> 1) + (p4 & 1) of quad qa, lg = (ch & 1) + 2 (p4 >> 1),
+// at 16-byte unit ((m / 16) quads + qa) 4 + sl) 64 + 16 lg + m % 16; inside
+// it the octet's elements sit as pairs (0, 2), (4, 6), (1, 3), (5, 7).
+__device__ __forceinline__ size_t frag_half(uint32_t m, uint32_t k, uint32_t quads) {
+    const uint32_t cc = k / 8, e = k % 8, qa = cc / 16, ch = (cc % 16) / 4, p4 = cc % 4;
+    const uint32_t sl = 2 * (ch >> 1) + (p4 & 1), lg = (ch & 1) + 2 * (p4 >> 1);
+    const size_t u = (((size_t)(m / 16) * quads + qa) * 4 + sl) * 64 + 16 * lg + m % 16;
+    return u * 8 + (((e & 1) << 1) | (e >> 2)) * 2 + ((e >> 1) & 1);
+}
+
 // Sum over a full 64-lane wave; result in every lane.
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<WAVE>(v); }
 

@@ -13,6 +13,7 @@
 //     no host round trip and can be captured once into a HIP graph.
 // Every intermediate is rounded at the same points as the reference's
 // unfused kernels.
+#include <algorithm>
 #include <cstdlib>
 #include <vector>
 
@@ -80,8 +81,24 @@ struct lssm_engine {
     uint32_t* seq = nullptr;
     bool fuse_ssd = true;
     // decode batches from this many rows pack x once per linear (launch_mma_pack);
-    // LSSM_PACK_MIN_ROWS at creation overrides it
+    // LSSM_PACK_MIN_ROWS at creation overrides it; parts_min_rows is the same
+    // for the normalise-on-load path below (LSSM_PARTS_MIN_ROWS)
     uint32_t pack_min_rows = 8;
+    uint32_t parts_min_rows = 3;
+    // packed decode batches whose two linears both take the single-pass MFMA
+    // GEMV (and the partial counts it reads): out_proj also writes r(h w),
+    // w the next layer's norm weight, in that GEMV's fragment order with each
+    // row's sums of squares of h over every 16 columns (h_frag, h_part), the
+    // SSD step r(y w') likewise over every 32 (g_frag, g_part), and the
+    // linears scale their fp32 sums by the rows' 1 / rms, so no pack launch
+    // runs after the first layer's in_proj (which packs r(x w) likewise).
+    // LSSM_NOPACK at creation: 0 = off; 2 = a pack launch of r(x w) with one
+    // partial a row before every linear (the GEMV's scaling on its own)
+    int nopack = 1;
+    void* h_frag = nullptr;
+    void* g_frag = nullptr;
+    float* h_part = nullptr;
+    float* g_part = nullptr;
     // LSSM_FUSED_MIXER=1: out_proj in the same launch too (bit-identical; on
     // the 2.7B shape it measures ~3 % slower than a separate out_proj launch:
     // its two waits on other workgroups' words cost more than one kernel
@@ -173,16 +190,27 @@ struct lssm_engine {
                               (B >= 2 && gemv_mma_takes(B, proj, d_model, wfmt, act));
         const bool fused_out = (B <= 4 && gemv_max_rows(d_inner, wfmt, act) >= 1) ||
                                (B >= 2 && gemv_mma_takes(B, d_model, d_inner, wfmt, act));
-        // 8 rows or more: x is normalised and packed once per linear (into
-        // d_gn) instead of by every block of the MFMA GEMV, whose staging is
-        // issue-bound (below 8 rows the extra launch costs what it saves)
-        const uint32_t PACK_MIN_ROWS = pack_min_rows;
+        // x is normalised and packed once per linear (into d_gn) instead of by
+        // every block of the MFMA GEMV, whose staging is issue-bound: from 8
+        // rows (below that the extra launch costs what it saves), or from 3
+        // when both linears take the single-pass kernel with its partial sums
+        // of squares (frag_parts: one pack launch per step, not per linear;
+        // 2.7B at batch 4: 2573 against 2454 tok/s, batch 6: 3548 against 3230)
+        const bool mmx_in = d_model % 128 == 0 && gemv_mmx_takes(B, proj, d_model, wfmt, act);
+        const bool mmx_out = d_inner % 128 == 0 && gemv_mmx_takes(B, d_model, d_inner, wfmt, act);
+        const uint32_t np_h = gemv_mmx_parts(B, d_model, d_inner, wfmt, act);
+        const uint32_t np_g = ssd_step_parts(H, P, N, act);
+        const bool parts_ok = mmx_in && mmx_out && np_h != 0 && np_g != 0;
+        const uint32_t PACK_MIN_ROWS = nopack != 0 && parts_ok ? parts_min_rows : pack_min_rows;
         const bool pack_in = B >= PACK_MIN_ROWS && d_model % 128 == 0 && gemv_mma_takes(B, proj, d_model, wfmt, act);
         const bool pack_out = B >= PACK_MIN_ROWS && d_inner % 128 == 0 &&
                               gemv_mma_takes(B, d_model, d_inner, wfmt, act);
         // packed in the single-pass kernel's fragment order when it takes the call
-        const bool frag_in = pack_in && gemv_mmx_takes(B, proj, d_model, wfmt, act);
-        const bool frag_out = pack_out && gemv_mmx_takes(B, d_model, d_inner, wfmt, act);
+        const bool frag_in = pack_in && mmx_in;
+        const bool frag_out = pack_out && mmx_out;
+        // x = r(x w) in fragment order with partial sums of squares (nopack)
+        const bool frag_parts = nopack == 1 && frag_in && frag_out && parts_ok;
+        const bool raw_pack = nopack == 2 && frag_in && frag_out;
         fused_layers = 0;
         mixer_layers = 0;
         if (e == hipSuccess) e = trace_rows(0, d_hidden, B);
@@ -221,9 +249,22 @@ struct lssm_engine {
                     mixer_layers += out_done ? 1u : 0u;
                 }
                 if (!ssd_done && pack_in) {
-                    e = launch_mma_pack(st(), d_hidden, d_model, w.norm_w, RMS_EPS, B, d_model, wfmt, act, d_gn,
-                                        frag_in);
-                    a.g.xpack = d_gn;
+                    if (frag_parts && li > 0) {
+                        a.g.xpack = h_frag;                    // the previous out_proj's
+                        a.g.xpart = h_part;
+                        a.g.nparts = np_h;
+                    } else {
+                        // (the first layer of frag_parts packs r(x w) too: every
+                        // linear then rounds at the same point)
+                        const bool raw = raw_pack || frag_parts;
+                        e = launch_mma_pack(st(), d_hidden, d_model, w.norm_w, RMS_EPS, B, d_model, wfmt, act,
+                                            d_gn, frag_in, raw ? h_part : nullptr);
+                        a.g.xpack = d_gn;
+                        if (raw) {
+                            a.g.xpart = h_part;
+                            a.g.nparts = 4;
+                        }
+                    }
                 }
                 if (!ssd_done && e == hipSuccess) e = launch_inproj_decode(st(), a);
             } else {
@@ -246,16 +287,34 @@ struct lssm_engine {
                       (char*)d_xbc + (size_t)(d_inner + GN) * es, xbc, dt, dts, w.dt_bias, w.A_log,
                       w.D, d_g, d_inner, ssd_layer(li), B, 1, H, P, N, G, 1, DT_MIN, DT_MAX, 1u, act,
                       z, zs};
+            if (frag_parts) {
+                s.yfrag = g_frag;
+                s.ypart = g_part;
+                s.ynorm_w = w.mixer_norm_w;
+            }
             if (!ssd_done) e = launch_ssd_step(st(), s);
             if (e != hipSuccess) break;
             if (out_done) continue;
             if (fused_out) {
                 GemvArgs g{d_g, d_inner, w.out_proj_w, w.out_proj_s, d_hidden, d_model, d_hidden,
                            w.mixer_norm_w, RMS_EPS, B, d_model, d_inner, wfmt, act, LSSM_EPI_ADD};
-                if (pack_out) {
+                if (frag_parts) {
+                    g.xpack = g_frag;                          // the SSD step's
+                    g.xpart = g_part;
+                    g.nparts = np_g;
+                    if (li + 1 < cfg.n_layer) {                // for the next in_proj
+                        g.yfrag = h_frag;
+                        g.ypart = h_part;
+                        g.ynorm_w = layers[li + 1].norm_w;
+                    }
+                } else if (pack_out) {
                     e = launch_mma_pack(st(), d_g, d_inner, w.mixer_norm_w, RMS_EPS, B, d_inner, wfmt, act, d_gn,
-                                        frag_out);
+                                        frag_out, raw_pack ? g_part : nullptr);
                     g.xpack = d_gn;
+                    if (raw_pack) {
+                        g.xpart = g_part;
+                        g.nparts = 4;
+                    }
                 }
                 if (e == hipSuccess) e = launch_gemv(st(), g);
             } else {
@@ -500,14 +559,29 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     const size_t xfer_bytes = (size_t)cfg->n_layer * e->xfer_words() * sizeof(uint64_t);
     A((void**)&e->xfer, xfer_bytes);
     A((void**)&e->seq, 256);
+    // rows up to the next multiple of 16 (the GEMV's row tiles; rows past the
+    // batch are read and their results dropped)
+    const size_t R16 = (size_t)(max_batch + 15) / 16 * 16;
+    const size_t hpb = R16 * std::max<size_t>(e->d_model / 16, 4) * sizeof(float);
+    const size_t gpb = R16 * std::max<size_t>(d_inner / 32, 4) * sizeof(float);
+    A(&e->h_frag, R16 * e->d_model * es);
+    A(&e->g_frag, R16 * d_inner * es);
+    A((void**)&e->h_part, hpb);
+    A((void**)&e->g_part, gpb);
     if (rc == LSSM_OK) {
         hipError_t err = hipMemsetAsync(e->xfer, 0, xfer_bytes, ctx->stream);
         if (err == hipSuccess) err = hipMemsetAsync(e->seq, 0, 256, ctx->stream);
+        if (err == hipSuccess) err = hipMemsetAsync(e->h_frag, 0, R16 * e->d_model * es, ctx->stream);
+        if (err == hipSuccess) err = hipMemsetAsync(e->g_frag, 0, R16 * d_inner * es, ctx->stream);
+        if (err == hipSuccess) err = hipMemsetAsync(e->h_part, 0, hpb, ctx->stream);
+        if (err == hipSuccess) err = hipMemsetAsync(e->g_part, 0, gpb, ctx->stream);
         if (err != hipSuccess) rc = set_error(LSSM_EDEVICE, "engine_create: %s", hipGetErrorString(err));
     }
     if (const char* v = getenv("LSSM_FUSED_SSD")) e->fuse_ssd = v[0] != '0';
     if (const char* v = getenv("LSSM_FUSED_MIXER")) e->fuse_mixer = v[0] == '1';
     if (const char* v = getenv("LSSM_PACK_MIN_ROWS")) e->pack_min_rows = (uint32_t)strtoul(v, nullptr, 10);
+    if (const char* v = getenv("LSSM_PARTS_MIN_ROWS")) e->parts_min_rows = (uint32_t)strtoul(v, nullptr, 10);
+    if (const char* v = getenv("LSSM_NOPACK")) e->nopack = (int)strtol(v, nullptr, 10);
     if (rc != LSSM_OK) {
         delete e;
         return rc;

@@ -31,6 +31,12 @@ struct GemvCore {
     // the MFMA decode GEMV only: x already normalised and packed in its
     // staging order ([M][K / 2] dwords, launch_mma_pack), or null
     const uint32_t* xp = nullptr;
+    // gemv_mmx only, with xp: when part is set, xp holds the rows raw (not
+    // normalised) in fragment order, their sums of squares are the `nparts`
+    // partial sums of each row in part ([rows][nparts], added in order) and
+    // the norm weight is norm_w
+    const float* part = nullptr;
+    uint32_t nparts = 0;
 };
 
 template <int FMT, typename T> struct Fmt;

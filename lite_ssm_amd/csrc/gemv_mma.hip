@@ -536,7 +536,59 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
 // ---------------------------------------------------------------------------
 constexpr int MMX_MAXW = 8;                      // waves per block: the K split
 
-template <int FMT, typename T, int CT, int RT, int QPW, int DR, class Epi>
+// x raw in fragment order (NX): the rows' partial sums of squares are read by
+// 16 lanes a row, 16 x 4 floats a step (at most this many partials a row)
+constexpr uint32_t MMX_MAXPARTS = GEMV_MAX_XPARTS;
+static_assert(MMX_MAXPARTS % 64 == 0, "16 lanes x float4 per step");
+
+// Epilogue h = r(res + r(acc)) (res may be y) that also writes r(h nw) in
+// fragment order for the next single-pass GEMV (nw: the norm weight of the
+// RMSNorm in front of it) and returns h^2: the kernel adds each row's 16
+// values of a tile and hands the sum to put_part.
+template <typename T> struct EpiResFrag {
+    static constexpr bool kParts = true;
+    T* y;
+    uint32_t y_stride;
+    const T* res;
+    T* frag;
+    float* part;
+    const T* nw;
+    uint32_t quads, nparts;                    // of the next GEMV's x (K = N here)
+    struct Pre {
+        uint32_t r, w;
+    };
+    __device__ __forceinline__ void pin() const {
+        pin_arg(y);
+        pin_arg(y_stride);
+        pin_arg(res);
+        pin_arg(frag);
+        pin_arg(part);
+        pin_arg(nw);
+        pin_arg(quads);
+        pin_arg(nparts);
+    }
+    __device__ __forceinline__ Pre prefetch(int m, uint32_t n) const {
+        return Pre{raw_at(res + ((uint32_t)m * y_stride + n)), raw_at(nw + n)};
+    }
+    __device__ __forceinline__ float store(uint32_t m, uint32_t n, float acc, const Pre& p) const {
+        const T h = from_f<T>(f_of_raw<T>(p.r) + rnd<T>(acc));
+        const float v = to_f(h);
+        y[(size_t)m * y_stride + n] = h;
+        frag[frag_half(m, n, quads)] = from_f<T>(v * f_of_raw<T>(p.w));
+        return v * v;
+    }
+    __device__ __forceinline__ void put_part(uint32_t m, uint32_t tile, float q) const {
+        part[(size_t)m * nparts + tile] = q;
+    }
+};
+template <class E, class = void> struct epi_parts {
+    static constexpr bool value = false;
+};
+template <class E> struct epi_parts<E, decltype((void)E::kParts)> {
+    static constexpr bool value = E::kParts;
+};
+
+template <int FMT, typename T, int CT, int RT, int QPW, int DR, bool NX, class Epi>
 __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi epi, uint32_t M) {
     using P = Mma<FMT, T>;
     using F = Fmt<FMT, T>;
@@ -559,6 +611,31 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
     // so each of these loads reads 1 KiB of consecutive bytes
     const u32x4* xf = reinterpret_cast<const u32x4*>(c.xp);
     const uint32_t quads = K / P::QK;
+
+    // NX (x = r(x_raw w), not scaled by the rows' 1 / rms): the block's
+    // rows' partial sums of squares of x_raw (16 lanes a row, NT / 16 rows a
+    // pass, two passes at most) are requested before anything else, reduced
+    // once the x and weight requests are out (loads return in issue order),
+    // and the rows' 1 / rms left in LDS behind the epilogue's partial-sum
+    // area, where the epilogue (after its barrier) scales the sums by them
+    constexpr uint32_t NPV = MMX_MAXPARTS / 64;                // float4 per lane and row
+    [[maybe_unused]] floatx4 pv[2][NPV];
+    const uint32_t NT0 = blockDim.x;
+    [[maybe_unused]] float* rrl = reinterpret_cast<float*>(mm_lds + KS * RT * CT * WAVE * 4);
+    if constexpr (NX) {
+        const uint32_t np = c.nparts, rpp = NT0 / 16;          // rows per pass
+        const uint32_t r0 = threadIdx.x / 16, l16 = threadIdx.x % 16;
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) {
+            const uint32_t r = min(r0 + ps * rpp, (uint32_t)(16 * RT) - 1);
+            const floatx4* pr = reinterpret_cast<const floatx4*>(c.part + (size_t)r * np);
+#pragma unroll
+            for (uint32_t j = 0; j < NPV; ++j) {
+                const uint32_t f = l16 + 16 * j;               // float4 index in the row
+                pv[ps][j] = 4 * f < np ? pr[f] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    }
     // x of XD quads in flight (a ring): as many as the registers left by the
     // weights and sums allow, at least two
     constexpr int XD = CT == 1 ? (QPW < (RT == 2 ? 4 : 8) ? QPW : (RT == 2 ? 4 : 8))
@@ -617,6 +694,24 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
                 wr[qd][t] = *reinterpret_cast<const u32x4*>(wp[t] + 64 * qd);
                 if constexpr (!SQ) sr[qd][t] = sp[t][qd];
             }
+    }
+
+    if constexpr (NX) {
+        const uint32_t rpp = NT0 / 16, r0 = threadIdx.x / 16;
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) {
+            // the row's partials in order within each lane, then over the 16
+            // lanes by a fixed butterfly
+            float t = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < NPV; ++j) t = t + pv[ps][j][0] + pv[ps][j][1] + pv[ps][j][2] + pv[ps][j][3];
+            t += __shfl_xor(t, 8);
+            t += __shfl_xor(t, 4);
+            t += __shfl_xor(t, 2);
+            t += __shfl_xor(t, 1);
+            const uint32_t r = r0 + ps * rpp;
+            if (threadIdx.x % 16 == 0 && r < 16u * RT) rrl[r] = 1.0f / sqrtf(t / (float)K + c.eps);
+        }
     }
 
     floatx4 acc[RT][CT];
@@ -718,12 +813,26 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
         const uint32_t o = threadIdx.x + NT * k;
-        if (o < NO) {
+        if (o < NO) {                                          // whole waves (NT, NO multiples of 64)
             float v = 0.0f;
             for (uint32_t ww = 0; ww < KS; ++ww) v += redf[ww * NO + o];
             uint32_t m, n;
             out_mn(o, m, n);
-            if (m < M && n < N && o / 256 % CT + tile0 < tiles) epi((int)m, n, v, pre[k]);
+            if constexpr (NX) v *= rrl[m];
+            const uint32_t tl = o / 256 % CT + tile0;
+            if constexpr (epi_parts<Epi>::value) {
+                float q = 0.0f;
+                if (m < M && n < N && tl < tiles) q = epi.store(m, n, v, pre[k]);
+                // a wave holds 4 rows (lane % 4) x the tile's 16 columns
+                // (lane / 4 % 16): the row sums by a fixed butterfly
+                q += __shfl_xor(q, 4);
+                q += __shfl_xor(q, 8);
+                q += __shfl_xor(q, 16);
+                q += __shfl_xor(q, 32);
+                if (lane < 4 && tl < tiles) epi.put_part(m, tl, q);
+            } else {
+                if (m < M && n < N && tl < tiles) epi((int)m, n, v, pre[k]);
+            }
         }
     }
 }
@@ -783,13 +892,21 @@ template <int FMT, typename T> bool mmx_plan(uint32_t M, uint32_t N, uint32_t K,
 
 template <int FMT, typename T, int CT, int RT, int QPW, class Epi, int DR = 0>
 hipError_t mmx_run(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, const MmxPlan& p) {
-    auto k = gemv_mmx_kernel<FMT, T, CT, RT, QPW, DR, Epi>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)MM_LDS_MAX);
-    if (attr != hipSuccess) return attr;
-    const uint32_t tiles = (c.N + 15) / 16;
-    k<<<(tiles + CT - 1) / CT, WAVE * p.ks, p.lds, s>>>(c, e, M);
-    return hipGetLastError();
+    auto go = [&](auto k, size_t lds) -> hipError_t {
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)MM_LDS_MAX);
+        if (attr != hipSuccess) return attr;
+        if (lds > MM_LDS_MAX) return hipErrorInvalidValue;
+        const uint32_t tiles = (c.N + 15) / 16;
+        k<<<(tiles + CT - 1) / CT, WAVE * p.ks, lds, s>>>(c, e, M);
+        return hipGetLastError();
+    };
+    if (c.part) {
+        // x = r(x_raw w): 32 rows' 1 / rms behind the epilogue area
+        if (c.nparts % 4 || c.nparts > MMX_MAXPARTS || (uintptr_t)c.part % 16) return hipErrorInvalidValue;
+        return go(gemv_mmx_kernel<FMT, T, CT, RT, QPW, DR, true, Epi>, p.lds + 32 * sizeof(float));
+    }
+    return go(gemv_mmx_kernel<FMT, T, CT, RT, QPW, DR, false, Epi>, p.lds);
 }
 
 template <int FMT, typename T, int CT, int RT, class Epi>
@@ -974,6 +1091,10 @@ bool try_mma(hipStream_t s, const GemvCore& c, const Epi& e, uint32_t M, int wfm
             err = mmx_go<FMT, T, Epi>(s, c, e, M, q);
             return true;
         }
+        if (c.part) {                                          // raw x: only the single-pass kernel
+            err = hipErrorInvalidValue;
+            return true;
+        }
         err = c.xp ? mma_shape<FMT, T, true, true, Epi>(s, c, e, M, p)
                    : mma_shape<FMT, T, true, false, Epi>(s, c, e, M, p);
         return true;
@@ -998,7 +1119,7 @@ template <typename T> bool mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfm
 // rows up to the next multiple of 16, and rows past M are zeros.
 template <int FMT, typename T, bool FRAG>
 __global__ __launch_bounds__(1024) void mma_pack_kernel(const T* x, uint32_t x_stride, const T* nw, float eps,
-                                                        uint32_t K, uint32_t M, uint32_t* out) {
+                                                        uint32_t K, uint32_t M, uint32_t* out, float* part) {
     // one octet per thread (blockDim.x >= K / 8), x and w read once
     __shared__ float red[1024 / WAVE];
     const uint32_t m = blockIdx.x, KO = K / 8, cc = threadIdx.x;
@@ -1021,12 +1142,16 @@ __global__ __launch_bounds__(1024) void mma_pack_kernel(const T* x, uint32_t x_s
     float t = 0.0f;
     for (uint32_t i = 0; i < nwv; ++i) t += red[i];
     const float rr = 1.0f / sqrtf(t / (float)K + eps);
+    // part: x w without 1 / rms, the sum of squares to part[4 m]
+    const bool raw = FRAG && part != nullptr;
+    if (raw && threadIdx.x < 4) part[4 * m + threadIdx.x] = threadIdx.x == 0 ? t : 0.0f;
     if (!live) return;
+    const float sc = raw ? 1.0f : rr;
     float v[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        v[2 * e] = lo_f<T>(xv[e]) * lo_f<T>(nv[e]) * rr;
-        v[2 * e + 1] = hi_f<T>(xv[e]) * hi_f<T>(nv[e]) * rr;
+        v[2 * e] = lo_f<T>(xv[e]) * lo_f<T>(nv[e]) * sc;
+        v[2 * e + 1] = hi_f<T>(xv[e]) * hi_f<T>(nv[e]) * sc;
     }
     u32x4 pk;
 #pragma unroll
@@ -1050,16 +1175,17 @@ __global__ __launch_bounds__(1024) void mma_pack_kernel(const T* x, uint32_t x_s
 }  // namespace
 
 hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, const void* norm_w, float eps,
-                           uint32_t M, uint32_t K, int wfmt, int act, void* out, bool frag) {
+                           uint32_t M, uint32_t K, int wfmt, int act, void* out, bool frag, float* part) {
     if (M == 0 || K % 128 != 0 || K > 8192 || (uintptr_t)x % 16 || (x_stride * 2u) % 16 ||
         (uintptr_t)norm_w % 16 || (uintptr_t)out % 16)
         return hipErrorInvalidValue;
     if (frag && (wfmt != LSSM_W_Q4_G64 || act != LSSM_BF16)) return hipErrorInvalidValue;
+    if (part && !frag) return hipErrorInvalidValue;
     const uint32_t nt = (K / 8 + WAVE - 1) / WAVE * WAVE;      // one octet per thread
     if (frag) {
         mma_pack_kernel<LSSM_W_Q4_G64, bf16, true><<<(M + 15) / 16 * 16, nt, 0, s>>>(
             static_cast<const bf16*>(x), x_stride, static_cast<const bf16*>(norm_w), eps, K, M,
-            static_cast<uint32_t*>(out));
+            static_cast<uint32_t*>(out), part);
         return hipGetLastError();
     }
     hipError_t err = hipErrorInvalidValue;
@@ -1069,7 +1195,7 @@ hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, cons
             constexpr int FMT = decltype(ft)::value;
             mma_pack_kernel<FMT, T, false><<<M, nt, 0, s>>>(static_cast<const T*>(x), x_stride,
                                                              static_cast<const T*>(norm_w), eps, K, M,
-                                                             static_cast<uint32_t*>(out));
+                                                             static_cast<uint32_t*>(out), nullptr);
             err = hipGetLastError();
             return true;
         });
@@ -1085,6 +1211,14 @@ bool gemv_mmx_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
     return mmx_plan<LSSM_W_Q4_G64, bf16>(M, N, K, p);
 }
 
+uint32_t gemv_mmx_parts(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
+    if (act != LSSM_BF16 || wfmt != LSSM_W_Q4_G64 || mmx_disabled()) return 0;
+    MmxPlan p;
+    if (!mmx_plan<LSSM_W_Q4_G64, bf16>(M, N, K, p) || p.ct != 1) return 0;
+    const uint32_t np = (N + 15) / 16;
+    return N % 128 == 0 && np % 4 == 0 && np <= MMX_MAXPARTS ? np : 0;
+}
+
 bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
     if (act == LSSM_F16) return mma_takes<f16>(M, N, K, wfmt);
     if (act == LSSM_BF16) return mma_takes<bf16>(M, N, K, wfmt);
@@ -1092,9 +1226,27 @@ bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act) {
 }
 
 bool launch_gemv_mma(hipStream_t s, const GemvArgs& a, hipError_t& err) {
-    if (a.M < 2) return false;
+    if (a.M < 2 && !a.yfrag) return false;
     GemvCore c{a.x, a.x_stride, (const uint8_t*)a.w, (const uint16_t*)a.s, a.norm_w, a.eps, a.N, a.K, 1.0f / (float)a.K};
     c.xp = static_cast<const uint32_t*>(a.xpack);
+    c.part = a.xpart;
+    c.nparts = a.nparts;
+    if (a.yfrag) {
+        // the rows also in fragment order with their partial sums of squares:
+        // residual add, one tile a block (gemv_mmx_parts)
+        const uint32_t np = gemv_mmx_parts(a.M, a.N, a.K, a.wfmt, a.act);
+        MmxPlan p;
+        err = hipErrorInvalidValue;
+        if (np == 0 || a.epi != LSSM_EPI_ADD || !a.res || !a.ypart || !a.ynorm_w || !a.norm_w || !a.xpack ||
+            (uintptr_t)a.yfrag % 16 || (uintptr_t)a.ypart % 16 ||
+            !mmx_plan<LSSM_W_Q4_G64, bf16>(a.M, a.N, a.K, p) || !mma_aligned<bf16>(c, true))
+            return true;
+        EpiResFrag<bf16> e{(bf16*)a.y, a.y_stride, (const bf16*)a.res, (bf16*)a.yfrag, a.ypart,
+                             (const bf16*)a.ynorm_w, a.N / 128, np};
+        err = p.rt == 1 ? mmx_q<LSSM_W_Q4_G64, bf16, 1, 1, EpiResFrag<bf16>>(s, c, e, a.M, p)
+                        : mmx_q<LSSM_W_Q4_G64, bf16, 1, 2, EpiResFrag<bf16>>(s, c, e, a.M, p);
+        return true;
+    }
     auto go = [&](auto tag) -> bool {
         using T = decltype(tag);
         EpiPlain<T> e{(T*)a.y, a.y_stride, (const T*)a.res, a.epi};
@@ -1110,6 +1262,8 @@ bool launch_inproj_decode_mma(hipStream_t s, const InprojDecodeArgs& a, hipError
     if (g.M < 2) return false;
     GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
     c.xp = static_cast<const uint32_t*>(g.xpack);
+    c.part = g.xpart;
+    c.nparts = g.nparts;
     auto go = [&](auto tag) -> bool {
         using T = decltype(tag);
         EpiInproj<T> e{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,

@@ -130,6 +130,19 @@ struct GemvArgs {
     // x rows as launch_mma_pack wrote them (norm_w applied), or null; used by
     // the MFMA decode GEMV, which then copies instead of normalising
     const void* xpack = nullptr;
+    // with xpack in fragment order: xpack holds r(x norm_w) without the
+    // rows' 1 / rms, which the GEMV forms from their partial sums of squares
+    // of x ([rows][nparts], added in order) and applies to its fp32 sums;
+    // null: xpack is normalised
+    const float* xpart = nullptr;
+    uint32_t nparts = 0;
+    // epi == LSSM_EPI_ADD, single-pass MFMA GEMV only (gemv_mmx_parts): the
+    // output rows h also as r(h ynorm_w) in fragment order for the next GEMV
+    // (yfrag, ceil(M / 16) * 16 rows of N) and each row's sum of squares of h
+    // over every 16 columns (ypart, [rows][N / 16]); null: y only
+    void* yfrag = nullptr;
+    float* ypart = nullptr;
+    const void* ynorm_w = nullptr;
 };
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a);
 // Rows of x one GEMV launch can take for this K / format (0 = none), with
@@ -185,8 +198,18 @@ struct SsdArgs {
     float* seg = nullptr;
     // set by the launcher: segments per sequence and chunks per segment
     uint32_t nseg = 1, seg_chunks = 0;
+    // decode step, bf16 with gate, H * P a multiple of 128 (ssd_step_parts):
+    // Y rows also as r(Y ynorm_w) in the single-pass MFMA GEMV's fragment
+    // order (yfrag, ceil(batch / 16) * 16 rows) and each row's sum of squares
+    // of Y over every 32 elements (ypart, [rows][H P / 32]); null: Y only
+    void* yfrag = nullptr;
+    float* ypart = nullptr;
+    const void* ynorm_w = nullptr;
 };
 hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a);
+// Partials per row a decode step with SsdArgs::yfrag writes (H P / 32), or 0
+// when it cannot.
+uint32_t ssd_step_parts(uint32_t H, uint32_t P, uint32_t N, int act);
 hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a);
 inline size_t ssd_gram_floats(uint32_t batch, uint32_t L, uint32_t G) {
     return (size_t)batch * ((L + 63) / 64) * G * 64 * 64;
@@ -271,10 +294,20 @@ bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);
 // pass for all blocks of the GEMV launch that follows (GemvArgs::xpack).
 hipError_t launch_mma_pack(hipStream_t s, const void* x, uint32_t x_stride, const void* norm_w,
                            float eps, uint32_t M, uint32_t K, int wfmt, int act, void* out,
-                           bool frag = false);
+                           bool frag = false, float* part = nullptr);
+// (with frag and part set, the rows are written as r(x norm_w), without
+// 1 / rms, and row m's sum of squares goes to part[4 m], zeros to part[4 m +
+// 1 .. 4 m + 3]: four partials a row, for the GEMV that scales its sums by
+// 1 / rms (GemvArgs::xpart); rows up to ceil(M / 16) * 16)
 // The MFMA decode GEMV takes (M, N, K) in its single-pass form, which reads x
 // packed in fragment order (launch_mma_pack with frag = true; the buffer then
 // holds ceil(M / 16) * 16 rows).
 bool gemv_mmx_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);
+// Partials per row (N / 16) the single-pass MFMA GEMV writes for (M, N, K)
+// with GemvArgs::yfrag, or 0 when it cannot (another plan, or a count the
+// GEMV that reads them does not take).
+uint32_t gemv_mmx_parts(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);
+// Most partial sums of squares a row the single-pass MFMA GEMV reads.
+constexpr uint32_t GEMV_MAX_XPARTS = 256;
 
 }  // namespace lssm

@@ -43,15 +43,28 @@ template <typename T> __device__ __forceinline__ float f_of(uint32_t r) {
     else return __uint_as_float(r);
 }
 
-template <typename T, int F, bool GATE>
-__global__ __launch_bounds__(ST_NT) void ssd_step_kernel(SsdArgs a) {
+// FRAG (bf16, gate; the decode batches whose out_proj normalises on load):
+// blocks of four waves own 32 consecutive rows j = h P + p of the flattened
+// (H, P) (H P a multiple of 128), write r(y w) (w = a.ynorm_w, the norm
+// weight in front of out_proj) in the single-pass MFMA GEMV's fragment order
+// (a.yfrag) and the 32 values' sum of squares of y to a.ypart[b][blockIdx.x].
+template <typename T, int F, bool GATE, bool FRAG = false>
+__global__ __launch_bounds__(FRAG ? 4 * ST_NT : ST_NT) void ssd_step_kernel(SsdArgs a) {
     typedef T T4 __attribute__((ext_vector_type(4)));
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     const uint32_t P = a.P, N = a.N;
-    const uint32_t PS = (P + ST_RB - 1) / ST_RB;
-    const uint32_t h = blockIdx.x / PS, ps = blockIdx.x % PS, b = blockIdx.y;
-    const uint32_t p = ps * ST_RB + threadIdx.x / ST_NV;
-    if (p >= P) return;                               // whole 8-lane row groups exit together
+    const uint32_t b = blockIdx.y;
+    uint32_t h, p;
+    if constexpr (FRAG) {
+        const uint32_t j = blockIdx.x * (4 * ST_RB) + threadIdx.x / ST_NV;
+        h = j / P;
+        p = j % P;
+    } else {
+        const uint32_t PS = (P + ST_RB - 1) / ST_RB;
+        h = blockIdx.x / PS;
+        p = (blockIdx.x % PS) * ST_RB + threadIdx.x / ST_NV;
+        if (p >= P) return;                           // whole 8-lane row groups exit together
+    }
     const uint32_t g = h / (a.H / a.G);
     const uint32_t lr = threadIdx.x % ST_NV;
     f32x4* S = reinterpret_cast<f32x4*>(a.state + (((size_t)b * a.H + h) * P + p) * N);
@@ -73,6 +86,7 @@ __global__ __launch_bounds__(ST_NT) void ssd_step_kernel(SsdArgs a) {
     const uint32_t dtr = raw_of((const T*)a.dt + (size_t)b * a.dt_stride + h);
     const uint32_t dbr = raw_of((const T*)a.dt_bias + h);
     const uint32_t dr = raw_of(a.has_D ? (const T*)a.D + h : Xp);   // value unused without D
+    [[maybe_unused]] const uint32_t nwr = FRAG ? raw_of((const T*)a.ynorm_w + h * P + p) : 0u;
 
     // dt = clamp(softplus(dt_raw + dt_bias)), decay = e^{A dt} (ssd_step.metal:55-66)
     const float xv = f_of<T>(xr);
@@ -95,10 +109,28 @@ __global__ __launch_bounds__(ST_NT) void ssd_step_kernel(SsdArgs a) {
         ys += fmaf(to_f(cv[f].w), t.w, fmaf(to_f(cv[f].z), t.z, fmaf(to_f(cv[f].x), t.x, to_f(cv[f].y) * t.y)));
     }
     ys = group_sum<ST_NV>(ys);
+    float q = 0.0f;
     if (lr == 0) {
         float y = rnd<T>(fmaf(a.has_D ? f_of<T>(dr) : 0.0f, xv, ys));
         if constexpr (GATE) y = silu_fast(f_of<T>(zr)) * y;
-        ((T*)a.Y)[(size_t)b * a.y_stride + (size_t)h * P + p] = from_f<T>(y);
+        const T yr = from_f<T>(y);
+        ((T*)a.Y)[(size_t)b * a.y_stride + (size_t)h * P + p] = yr;
+        if constexpr (FRAG) {
+            const float yv = to_f(yr);
+            const float wv = f_of<T>(nwr);
+            static_cast<T*>(a.yfrag)[frag_half(b, h * P + p, a.H * P / 128)] = from_f<T>(yv * wv);
+            q = yv * yv;
+        }
+    }
+    if constexpr (FRAG) {
+        // the wave's 8 rows (lanes 8 i), then the 4 waves in order
+        __shared__ float red[4];
+        q += __shfl_xor(q, 8);
+        q += __shfl_xor(q, 16);
+        q += __shfl_xor(q, 32);
+        if (threadIdx.x % WAVE == 0) red[threadIdx.x / WAVE] = q;
+        __syncthreads();
+        if (threadIdx.x == 0) a.ypart[(size_t)b * gridDim.x + blockIdx.x] = red[0] + red[1] + red[2] + red[3];
     }
 }
 
@@ -1019,6 +1051,21 @@ hipError_t step_go(hipStream_t s, const SsdArgs& a) {
     const size_t v4 = 4 * sizeof(T);
     const bool vec = ((uintptr_t)a.state % 16 == 0) && ((uintptr_t)a.B % v4 == 0) &&
                      ((uintptr_t)a.C % v4 == 0) && (a.b_stride % 4 == 0) && (a.c_stride % 4 == 0);
+    if (a.yfrag) {
+        if constexpr (__is_same(T, bf16) && GATE) {
+            if (!vec || ssd_step_parts(a.H, a.P, a.N, a.act) == 0 || !a.ypart || !a.ynorm_w ||
+                (uintptr_t)a.yfrag % 16)
+                return hipErrorInvalidValue;
+            const dim3 gf(a.H * a.P / (4 * ST_RB), a.batch);
+            if (a.N == 128) ssd_step_kernel<T, 4, GATE, true><<<gf, 4 * ST_NT, 0, s>>>(a);
+            else if (a.N == 64) ssd_step_kernel<T, 2, GATE, true><<<gf, 4 * ST_NT, 0, s>>>(a);
+            else if (a.N == 256) ssd_step_kernel<T, 8, GATE, true><<<gf, 4 * ST_NT, 0, s>>>(a);
+            else ssd_step_kernel<T, 1, GATE, true><<<gf, 4 * ST_NT, 0, s>>>(a);
+            return hipGetLastError();
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
     const dim3 grid(a.H * ((a.P + ST_RB - 1) / ST_RB), a.batch);
     if (vec && a.N == 128) ssd_step_kernel<T, 4, GATE><<<grid, ST_NT, 0, s>>>(a);
     else if (vec && a.N == 64) ssd_step_kernel<T, 2, GATE><<<grid, ST_NT, 0, s>>>(a);
@@ -1029,6 +1076,12 @@ hipError_t step_go(hipStream_t s, const SsdArgs& a) {
 }
 
 }  // namespace
+
+uint32_t ssd_step_parts(uint32_t H, uint32_t P, uint32_t N, int act) {
+    const uint32_t HP = H * P;
+    const bool n_ok = N == 32 || N == 64 || N == 128 || N == 256;
+    return act == LSSM_BF16 && n_ok && HP % 128 == 0 && HP / 32 <= GEMV_MAX_XPARTS ? HP / 32 : 0;
+}
 
 hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a) {
     if (a.batch == 0 || a.H == 0) return hipSuccess;
