@@ -105,6 +105,56 @@ def test_engine_graph_replay_matches_eager(ctx):
     eng.close()
 
 
+def test_engine_batched_graph_and_stale_rows(ctx):
+    """Batched decode on the normalise-on-load path (int4-g64 bf16, 3 layers):
+    graph replay is bit-identical to eager steps, and a batch of 5 decoded after
+    a batch of 8 (whose rows 5..15 of the packed-x and partial-sum buffers then
+    hold stale values the GEMVs read and drop) gives the bits a fresh engine
+    gives."""
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-2.7b", O.BF16, O.W_Q4_G64, n_layer=3, vocab_size=1024, seed=31)
+    g = torch.Generator().manual_seed(9)
+    ids8 = torch.randint(0, sh.vocab_size, (8, 24), generator=g, dtype=torch.int32).cuda()
+    ids5 = torch.randint(0, sh.vocab_size, (5, 24), generator=g, dtype=torch.int32).cuda()
+
+    def run5(eng):
+        tok = torch.zeros(5, dtype=torch.int32, device="cuda")
+        eng.prefill(ids5, tok)
+        for _ in range(3):
+            eng.decode(tok, tok)
+        return eng.logits(5), tok.clone()
+
+    fresh = Engine(ctx, m, max_batch=8, max_seq=24)
+    try:
+        lg_fresh, tok_fresh = run5(fresh)
+    finally:
+        fresh.close()
+    eng = Engine(ctx, m, max_batch=8, max_seq=24)
+    try:
+        tok = torch.zeros(8, dtype=torch.int32, device="cuda")
+        eng.prefill(ids8, tok)
+        t_e = tok.clone()
+        for _ in range(4):
+            eng.decode(t_e, t_e)
+        conv_e, ssd_e = eng.state()
+        conv_e, ssd_e = conv_e.clone(), ssd_e.clone()
+        lg_e = eng.logits(8)
+        eng.reset()
+        eng.prefill(ids8, tok)
+        t_g = tok.clone()
+        eng.decode_graph(t_g, t_g, 4)
+        conv_g, ssd_g = eng.state()
+        assert torch.equal(t_g, t_e)
+        assert torch.equal(ssd_g, ssd_e) and torch.equal(conv_g, conv_e)
+        assert torch.equal(eng.logits(8), lg_e)
+        eng.reset()
+        lg5, tok5 = run5(eng)
+        assert torch.equal(tok5, tok_fresh)
+        assert torch.equal(lg5, lg_fresh), "batch-5 logits depend on the earlier batch-8 rows"
+    finally:
+        eng.close()
+
+
 def test_engine_batch8_decode(ctx):
     """Batch 8: prefill on the MFMA GEMMs, decode on the MFMA GEMV (exact
     dequantization, as the oracle's and the reference's decode)."""
@@ -186,7 +236,9 @@ def test_engine_8b_widths_packed_decode(ctx, B):
         eng.close()
 
 
-@pytest.mark.parametrize("name,B", [("mamba2-2.7b", 4), ("mamba2-2.7b", 8), ("mamba2-2.7b", 24), ("mamba2-8b", 16)])
+@pytest.mark.parametrize("name,B", [("mamba2-2.7b", 3), ("mamba2-2.7b", 4), ("mamba2-2.7b", 8),
+                                    ("mamba2-2.7b", 17), ("mamba2-2.7b", 24), ("mamba2-2.7b", 32),
+                                    ("mamba2-8b", 16)])
 def test_engine_normalise_on_load_decode(ctx, monkeypatch, name, B):
     """Packed decode batches without the pack launches between layers: out_proj
     writes r(h w) (w: the next layer's norm weight) in the single-pass GEMV's
@@ -232,8 +284,8 @@ def test_engine_normalise_on_load_decode(ctx, monkeypatch, name, B):
     for mode in ("0", "2", "1"):
         for step in range(3):
             _check_logits(logits[mode][step], refs[step + 1], O.BF16, f"{name} b{B} mode {mode} decode {step}")
-    # (measured: 1.0000 after the first layer, >= 0.995 after the second,
-    # >= 0.95 after the third, where single-ulp flips have spread)
+    # (measured: 1.0000 after the first layer, >= 0.993 after the second,
+    # >= 0.93 after the third, where single-ulp flips have spread)
     for li in range(1, sh.n_layer + 1):
         same = float(np.mean(traces["1"][li] == traces["2"][li]))
         print(f"hidden rows after layer {li - 1}: {same:.4f} of elements equal (modes 1, 2)", flush=True)
