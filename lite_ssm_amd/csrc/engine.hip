@@ -119,15 +119,29 @@ struct lssm_engine {
         return hipMemcpyAsync((char*)trace + (size_t)slot * n, h, n, hipMemcpyDeviceToDevice, st());
     }
 
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t graph_exec = nullptr;
+    // decode graphs of one step and of graph_unroll steps in a row (each
+    // graph launch costs a gap of ~8 us before its first kernel; steps are
+    // replayed unroll at a time, the rest one at a time).  2.7B batch 1: 1130
+    // tok/s at one step per launch, 1137 at 4, 1138 at 8; batch 8: 4497,
+    // 4511, 4435 (8-step graphs of the batched path measure slower).
+    // LSSM_GRAPH_UNROLL at creation overrides the count (1: one step a launch).
+    hipGraph_t graph[2] = {nullptr, nullptr};
+    hipGraphExec_t graph_exec[2] = {nullptr, nullptr};
+    uint32_t graph_unroll = 4;
     const int32_t* g_ids = nullptr;
     int32_t* g_next = nullptr;
     uint32_t g_batch = 0;
+    void drop_graphs() {
+        for (int i = 0; i < 2; ++i) {
+            if (graph_exec[i]) (void)hipGraphExecDestroy(graph_exec[i]);
+            if (graph[i]) (void)hipGraphDestroy(graph[i]);
+            graph_exec[i] = nullptr;
+            graph[i] = nullptr;
+        }
+    }
 
     ~lssm_engine() {
-        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
-        if (graph) (void)hipGraphDestroy(graph);
+        drop_graphs();
         for (void* p : allocs) (void)hipFree(p);
     }
 
@@ -581,6 +595,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     if (const char* v = getenv("LSSM_FUSED_MIXER")) e->fuse_mixer = v[0] == '1';
     if (const char* v = getenv("LSSM_PACK_MIN_ROWS")) e->pack_min_rows = (uint32_t)strtoul(v, nullptr, 10);
     if (const char* v = getenv("LSSM_PARTS_MIN_ROWS")) e->parts_min_rows = (uint32_t)strtoul(v, nullptr, 10);
+    if (const char* v = getenv("LSSM_GRAPH_UNROLL")) e->graph_unroll = (uint32_t)strtoul(v, nullptr, 10);
     if (const char* v = getenv("LSSM_NOPACK")) e->nopack = (int)strtol(v, nullptr, 10);
     if (rc != LSSM_OK) {
         delete e;
@@ -645,30 +660,45 @@ int lssm_engine_decode_graph(lssm_engine* e, const int32_t* ids, uint32_t batch,
     LSSM_REQUIRE(batch >= 1 && batch <= e->max_batch, "forward_step: batch out of range");
     LSSM_REQUIRE(ids && next_ids, "forward_step: null ids");
     hipStream_t s = e->ctx->stream;
-    if (!e->graph_exec || e->g_ids != ids || e->g_next != next_ids || e->g_batch != batch) {
-        if (e->graph_exec) {
-            (void)hipGraphExecDestroy(e->graph_exec);
-            e->graph_exec = nullptr;
-        }
-        if (e->graph) {
-            (void)hipGraphDestroy(e->graph);
-            e->graph = nullptr;
-        }
-        hipError_t err = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
-        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: begin capture");
-        hipError_t le = e->decode(ids, batch, next_ids);
-        err = hipStreamEndCapture(s, &e->graph);
-        if (le != hipSuccess) return engine_finish(e, le, "engine_decode_graph: capture");
-        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: end capture");
-        err = hipGraphInstantiate(&e->graph_exec, e->graph, nullptr, nullptr, 0);
-        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: instantiate");
+    if (e->g_ids != ids || e->g_next != next_ids || e->g_batch != batch) {
+        e->drop_graphs();
         e->g_ids = ids;
         e->g_next = next_ids;
         e->g_batch = batch;
     }
-    for (uint32_t i = 0; i < steps; ++i) {
-        hipError_t err = hipGraphLaunch(e->graph_exec, s);
-        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: launch");
+    // graph k of n steps, captured on first use
+    auto exec = [&](int k, uint32_t n) -> int {
+        if (e->graph_exec[k]) return LSSM_OK;
+        if (e->graph[k]) {                                     // left by a failed instantiation
+            (void)hipGraphDestroy(e->graph[k]);
+            e->graph[k] = nullptr;
+        }
+        hipError_t err = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: begin capture");
+        hipError_t le = hipSuccess;
+        for (uint32_t i = 0; i < n && le == hipSuccess; ++i) le = e->decode(ids, batch, next_ids);
+        err = hipStreamEndCapture(s, &e->graph[k]);
+        if (le != hipSuccess) return engine_finish(e, le, "engine_decode_graph: capture");
+        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: end capture");
+        err = hipGraphInstantiate(&e->graph_exec[k], e->graph[k], nullptr, nullptr, 0);
+        if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: instantiate");
+        return LSSM_OK;
+    };
+    const uint32_t U = e->graph_unroll > 1 ? e->graph_unroll : 1;
+    uint32_t left = steps;
+    if (U > 1 && left >= U) {
+        if (int rc = exec(1, U)) return rc;
+        for (; left >= U; left -= U) {
+            hipError_t err = hipGraphLaunch(e->graph_exec[1], s);
+            if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: launch");
+        }
+    }
+    if (left > 0) {
+        if (int rc = exec(0, 1)) return rc;
+        for (; left > 0; --left) {
+            hipError_t err = hipGraphLaunch(e->graph_exec[0], s);
+            if (err != hipSuccess) return engine_finish(e, err, "engine_decode_graph: launch");
+        }
     }
     return finish(e->ctx, "engine_decode_graph");
 }

@@ -82,15 +82,18 @@ def test_engine_graph_replay_matches_eager(ctx):
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     eng.prefill(ids, tok)
     conv0, ssd0 = eng.state()
-    # eager: 5 steps feeding back the engine's own greedy ids
+    # eager: 11 steps feeding back the engine's own greedy ids
     t_e = tok.clone()
     eager = []
-    for _ in range(5):
+    for _ in range(11):
         eng.decode(t_e, t_e)
         eager.append(int(t_e.item()))
     conv_e, ssd_e = eng.state()
     lg_e = eng.logits(1)
-    # graph: restore the post-prefill state, replay 5 steps
+    # graph: restore the post-prefill state, replay 5 steps one call at a
+    # time, then 6 in one call (launches of the unrolled graph of 4 steps by
+    # default and of the one-step graph); then, from the start again, 11 + 11
+    # steps against 11 more eager steps
     eng.reset()
     eng.prefill(ids, tok)
     t_g = tok.clone()
@@ -98,8 +101,24 @@ def test_engine_graph_replay_matches_eager(ctx):
     for _ in range(5):
         eng.decode_graph(t_g, t_g, 1)
         graph.append(int(t_g.item()))
+    eng.decode_graph(t_g, t_g, 6)
+    graph.append(int(t_g.item()))
+    eager = eager[:5] + [eager[-1]]
     conv_g, ssd_g = eng.state()
     assert graph == eager
+    assert torch.equal(ssd_g, ssd_e) and torch.equal(conv_g, conv_e)
+    assert torch.equal(eng.logits(1), lg_e)
+    for _ in range(11):
+        eng.decode(t_e, t_e)
+    conv_e, ssd_e = eng.state()
+    lg_e = eng.logits(1)
+    eng.reset()
+    eng.prefill(ids, tok)
+    t_g = tok.clone()
+    eng.decode_graph(t_g, t_g, 11)
+    eng.decode_graph(t_g, t_g, 11)
+    conv_g, ssd_g = eng.state()
+    assert torch.equal(t_g, t_e)
     assert torch.equal(ssd_g, ssd_e) and torch.equal(conv_g, conv_e)
     assert torch.equal(eng.logits(1), lg_e)
     eng.close()
