@@ -345,14 +345,29 @@ def cpu_baseline(O, L, m, sh, decode_steps, prefill_len):
 # ----------------------------------------------------------------------------- main
 def profile_kernel(L, torch, ctx, eng, m, sh):
     """Workload of the rocprofv3 --pmc runs: the dominant decode kernel over all
-    64 layers' weights and the engine's state slabs, 10 times, then a 256 MiB
-    device-to-device copy 10 times (the known-size reference that scales the
-    FETCH_SIZE / WRITE_SIZE counters)."""
+    64 layers' weights and the engine's state slabs, 10 times, the batch-1
+    out_proj launch over all layers 10 times, then a 256 MiB device-to-device
+    copy 10 times (the known-size reference that scales the FETCH_SIZE /
+    WRITE_SIZE counters)."""
     args, keep = fused_setup(L, torch, eng, m, sh)
     run = fused_launcher(L, ctx, sh, args)
     ctx.begin_batch()
     for _ in range(10):
         run()
+    ctx.commit_and_wait()
+    # then the batch-1 out_proj launch (RMSNorm + int4 GEMV + residual, the
+    # engine's second launch per layer) over every layer, 10 times, on the
+    # fused launches' gated outputs
+    hid, y, _ = keep
+    ctx.begin_batch()
+    for _ in range(10):
+        bad = 0
+        for li, Lw in enumerate(m.layers):
+            bad |= L.lib.lssm_norm_linear_decode(ctx.h, y[li].data_ptr(), Lw["mixer_norm_w"].data_ptr(), 1e-5,
+                                                 Lw["out_proj_w"].data_ptr(), Lw["out_proj_s"].data_ptr(),
+                                                 hid.data_ptr(), hid.data_ptr(), 1, sh.d_model, sh.d_inner,
+                                                 L.W_Q4_G64, L.BF16, L.EPI_ADD)
+        L.check(bad)
     ctx.commit_and_wait()
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
