@@ -433,10 +433,12 @@ def test_engine_fused_ssd_decode_bs1(ctx, tag, name, act, wfmt, over, mixer):
     L, sh, m, om = _setup(ctx, name, act, wfmt, **over)
     Lq = 40
     os.environ["LSSM_FUSED_MIXER"] = "1"
+    os.environ["LSSM_FUSED_SSD"] = "1"
     try:
         fused = Engine(ctx, m, max_batch=1, max_seq=Lq)
     finally:
         del os.environ["LSSM_FUSED_MIXER"]
+        del os.environ["LSSM_FUSED_SSD"]
     os.environ["LSSM_FUSED_SSD"] = "0"
     try:
         plain = Engine(ctx, m, max_batch=1, max_seq=Lq)
@@ -468,6 +470,30 @@ def test_engine_default_bs1_fuses_ssd_only(ctx):
     finally:
         fused.close()
         plain.close()
+
+
+def test_engine_default_bs1_small_model_three_launches(ctx):
+    """A model whose SSD step has work items for fewer than half the CUs (the
+    130M shape: 24 heads x 64 rows = 48 items of 32 rows) decodes batch 1 in
+    three launches per layer by default, within tolerance of the oracle."""
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-130m", O.F16, O.W_Q8_G32, n_layer=2, vocab_size=1024)
+    eng = Engine(ctx, m, max_batch=1, max_seq=16)
+    try:
+        ids = np.random.default_rng(3).integers(0, sh.vocab_size, (1, 16)).astype(np.int32)
+        nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        eng.prefill(torch.from_numpy(ids).cuda(), nxt)
+        conv, ssd = om.new_state(1)
+        ref = om.prefill(conv, ssd, ids)
+        tok = O.argmax(ref, O.F16)
+        for step in range(2):
+            eng.decode(torch.from_numpy(tok).cuda(), nxt)
+            assert eng.fused_layers() == (0, 0)
+            ref = om.decode(conv, ssd, tok)
+            _check_logits(eng.logits(1).float().cpu().numpy(), ref, O.F16, f"130m default decode {step}")
+            tok = O.argmax(ref, O.F16)
+    finally:
+        eng.close()
 
 
 def _fused_vs_plain(tag, sh, om, act, fused, plain, Lq, counts):
