@@ -533,11 +533,17 @@ __global__ __launch_bounds__(64 * mma_waves(CT, QPW)) void gemv_mma_kernel(GemvC
 // gemv_mma_kernel's and the partials are summed in wave order; the K split
 // (at most 8 waves here) can differ from that kernel's, so the two may round
 // the fp32 sum of an output differently.
+// With NX, x holds r(x w) without the rows' 1 / rms (written so by the kernel
+// before, with partial sums of squares of x: the out_proj epilogue EpiResFrag,
+// the SSD step, or launch_mma_pack with part); the block adds each row's
+// partials in a fixed order and scales its fp32 sums by 1 / rms in the
+// epilogue, where the reference scales x before rounding it (the same one
+// rounding of each input, at another point).
 // ---------------------------------------------------------------------------
 constexpr int MMX_MAXW = 8;                      // waves per block: the K split
 
-// x raw in fragment order (NX): the rows' partial sums of squares are read by
-// 16 lanes a row, 16 x 4 floats a step (at most this many partials a row)
+// NX: the rows' partial sums of squares are read by 16 lanes a row, 16 x 4
+// floats a step (at most this many partials a row)
 constexpr uint32_t MMX_MAXPARTS = GEMV_MAX_XPARTS;
 static_assert(MMX_MAXPARTS % 64 == 0, "16 lanes x float4 per step");
 
