@@ -356,11 +356,12 @@ def test_engine_2p7b_layer_shapes(ctx):
     eng.close()
 
 
-@pytest.mark.parametrize("B", [16, 5])
+@pytest.mark.parametrize("B", [16, 5, 40])
 def test_engine_2p7b_batched_decode(ctx, B):
     """Full-width 2.7B layers decoding B sequences at once on the MFMA GEMV
-    (in_proj: 3 tiles per block; out_proj: K 5120, 16 rows in two passes of
-    8), against the oracle's per-sequence GEMV-rule decode."""
+    (in_proj: 3 tiles per block; out_proj: K 5120; 40 rows: past the
+    single-pass kernel's 32, the staged kernel with a pack launch before each
+    linear), against the oracle's per-sequence GEMV-rule decode."""
     from lite_ssm_amd.model import Engine
     L, sh, m, om = _setup(ctx, "mamba2-2.7b", O.BF16, O.W_Q4_G64, n_layer=1, vocab_size=512, seed=13)
     Lq = 8
