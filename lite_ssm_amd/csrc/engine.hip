@@ -72,6 +72,8 @@ struct lssm_engine {
     void* argmax_scratch = nullptr;
     float* gram = nullptr;     // prefill: the chunks' C B^T tiles, shared by a group's heads
     float* seg = nullptr;      // prefill: the chunked scan's segment workspace
+    // prefill: the split-K slices of GEMMs whose grid leaves most CUs idle
+    float* gemm_ws = nullptr;
     // batch-1 decode: in_proj, the SSD step (and out_proj) in one launch
     // (tagged words of each layer's projection and gated SSD output; the tag
     // is a count of batch-1 steps the embedding advances, so consecutive uses
@@ -374,6 +376,8 @@ struct lssm_engine {
             if (e == hipSuccess && !fused) {
                 GemmArgs g{normed, d_model, w.in_proj_w, w.in_proj_s, projb, proj, nullptr, R, proj,
                            d_model, wfmt, act, LSSM_EPI_NONE, 1};
+                g.ws = gemm_ws;
+                g.ws_floats = GEMM_WS_FLOATS;
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
             }
             if (e != hipSuccess) break;
@@ -400,6 +404,8 @@ struct lssm_engine {
             if (e == hipSuccess) {
                 GemmArgs g{gn, d_inner, w.out_proj_w, w.out_proj_s, hidden, d_model, hidden, R, d_model,
                            d_inner, wfmt, act, LSSM_EPI_ADD, 1};
+                g.ws = gemm_ws;
+                g.ws_floats = GEMM_WS_FLOATS;
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
             }
         }
@@ -566,6 +572,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A(&e->argmax_scratch, (size_t)max_batch * 128 * 8);
     A((void**)&e->gram, ssd_gram_floats(max_batch, max_seq, G) * sizeof(float));
     A((void**)&e->seg, ssd_seg_floats() * sizeof(float));
+    A((void**)&e->gemm_ws, GEMM_WS_FLOATS * sizeof(float));
     if (e->short_fused()) {
         const size_t R16 = (size_t)max_batch * 16;
         A(&e->f_z, R16 * d_inner * es);

@@ -347,7 +347,9 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
     uint32_t tm, tn;
     xcd_tile(tm, tn);
     const uint32_t m0 = tm * G2M, n0 = tn * BN;
-    const uint32_t K = a.K, KT = K / G2K;
+    // split K (gridDim.z > 1, small grids): slice z takes steps z KT .. + KT
+    // and writes its fp32 sums to a.ws; K stays the row length of X and W
+    const uint32_t K = a.K, KT = K / G2K / gridDim.z, kz = blockIdx.z * KT * G2K;
     // a barrier without __syncthreads' release fence (which would wait for
     // every DMA in flight); the empty asm keeps memory operations in place
     auto barrier = [] {
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
             for (int j = 0; j < 4; ++j) {
                 const uint32_t sl = (lane % 8) ^ swz(8 * j + lane / 8);
                 const uint32_t n = min(n0 + 32 * q + 8 * j + lane / 8, a.N - 1);
-                wq[j] = (const char*)a.w + ((size_t)n * K + 8 * sl) * sizeof(T);
+                wq[j] = (const char*)a.w + ((size_t)n * K + kz + 8 * sl) * sizeof(T);
             }
             auto dma_w = [&](uint32_t kt) {
                 T* dst = Bs[kt % SB] + (32 * q) * G2K;
@@ -397,8 +399,9 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
             const uint32_t br = p / TPR, c0 = (p % TPR) * CPT;
             constexpr uint32_t GS = FMT == LSSM_W_Q4_G64 ? 64 : 32;
             const uint32_t nrow = min(n0 + br, a.N - 1);
-            const char* wq = (const char*)a.w + (size_t)nrow * (FMT == LSSM_W_Q8_G32 ? K : K / 2);
-            const uint16_t* sp = (const uint16_t*)a.s + (size_t)nrow * (K / GS);
+            const char* wq = (const char*)a.w + (size_t)nrow * (FMT == LSSM_W_Q8_G32 ? K : K / 2) +
+                             (FMT == LSSM_W_Q8_G32 ? kz : kz / 2);
+            const uint16_t* sp = (const uint16_t*)a.s + (size_t)nrow * (K / GS) + kz / GS;
             using R = WRaw<FMT>;
             auto load_w = [&](uint32_t kt, R (&r)[CPT]) {
 #pragma unroll
@@ -463,7 +466,7 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
     }
     const uint32_t as0 = lds_addr(&As[0][0]) + (XR * w) * G2K * (uint32_t)sizeof(T);
     auto dma_x = [&](uint32_t kt, int j0, int j1) {
-        const char* base = (const char*)a.x + (size_t)kt * G2K * sizeof(T);
+        const char* base = (const char*)a.x + ((size_t)kz + (size_t)kt * G2K) * sizeof(T);
         const uint32_t dst = as0 + (kt % 3) * (G2M * G2K * (uint32_t)sizeof(T));
         for (int j = j0; j < j1; ++j) lds_dma16_asm(base + xo[j], dst + 8 * j * G2K * (uint32_t)sizeof(T));
     };
@@ -534,6 +537,22 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
 
     // D layout of v_mfma_f32_32x32x*: element r of lane l is
     // row (r/4)*8 + (l/32)*4 + r%4, column l%32.
+    if (gridDim.z > 1) {
+        float* ws = a.ws + (size_t)blockIdx.z * a.M * a.N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t n = n0 + wn * 64 + j * 32 + lane % 32;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t m = m0 + wm * 128 + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + r % 4;
+                    if (m < a.M && n < a.N) ws[(size_t)m * a.N + n] = acc[i][j][r];
+                }
+            }
+        }
+        return;
+    }
     T* Y = (T*)a.y;
     const T* Rz = (const T*)a.res;
     const bool vec = a.y_stride % 8 == 0 && (uintptr_t)a.y % 16 == 0 &&
@@ -821,6 +840,40 @@ hipError_t go_skinny_mt(hipStream_t s, const GemmArgs& a, int upw) {
     return go_skinny<FMT, T, MT, 1>(s, a);
 }
 
+// The split slices' fp32 sums added in slice order, then gemm2_kernel's
+// epilogue: r(v), r(silu(v)) or r(res + r(v)).
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void gemm_split_sum_kernel(GemmArgs a, uint32_t S) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, MN = (size_t)a.M * a.N;
+    if (i >= MN) return;
+    float v = 0.0f;
+    for (uint32_t z = 0; z < S; ++z) v += a.ws[z * MN + i];
+    const uint32_t m = (uint32_t)(i / a.N), n = (uint32_t)(i % a.N);
+    const size_t yi = (size_t)m * a.y_stride + n;
+    if (EPI == LSSM_EPI_SILU) v = silu_f(v);
+    if (EPI == LSSM_EPI_ADD) v = to_f(((const T*)a.res)[yi]) + rnd<T>(v);
+    ((T*)a.y)[yi] = from_f<T>(v);
+}
+
+// K slices for a prefill GEMM whose 256 x 128 tiles would leave most CUs idle
+// (the 130M out_proj at 2048 rows: 48 tiles): as many as fill about half the
+// CUs, K / 64 divisible, the workspace large enough; 1 = no split.
+inline uint32_t gemm_split(const GemmArgs& a, uint32_t gs) {
+    static const bool off = [] {
+        const char* v = getenv("LSSM_GEMM_SPLIT");
+        return v && v[0] == '0';
+    }();
+    if (!a.ws || off) return 1;
+    const size_t narrow = (size_t)((a.M + G2M - 1) / G2M) * ((a.N + 127) / 128), cus = num_cus();
+    if (2 * narrow > cus) return 1;
+    uint32_t S = 1;
+    for (uint32_t c : {2u, 4u, 8u})
+        if (narrow * c <= cus && (a.K / G2K) % c == 0 && (a.K / c) % gs == 0 &&
+            (size_t)c * a.M * a.N <= a.ws_floats)
+            S = c;
+    return S;
+}
+
 template <int FMT, typename T>
 hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
     // decode batches: weights streamed once
@@ -854,6 +907,21 @@ hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
                 }
             }
         };
+        const uint32_t S = FMT == LSSM_W_DENSE ? 1u : gemm_split(a, FMT == LSSM_W_Q4_G64 ? 64u : 32u);
+        if (S > 1) {
+            // small grid: K in S slices, then the slices' sums (one launch)
+            dim3 grid((a.N + 127) / 128, mt, S);
+            gemm2_kernel<FMT, T, LSSM_EPI_NONE, 4><<<grid, 512, 0, s>>>(a);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            const unsigned nb = (unsigned)(((size_t)a.M * a.N + 255) / 256);
+            switch (a.epi) {
+                case LSSM_EPI_SILU: gemm_split_sum_kernel<T, LSSM_EPI_SILU><<<nb, 256, 0, s>>>(a, S); break;
+                case LSSM_EPI_ADD: gemm_split_sum_kernel<T, LSSM_EPI_ADD><<<nb, 256, 0, s>>>(a, S); break;
+                default: gemm_split_sum_kernel<T, LSSM_EPI_NONE><<<nb, 256, 0, s>>>(a, S); break;
+            }
+            return hipGetLastError();
+        }
         auto run_narrow = [&](const GemmArgs& g) {
             dim3 grid((g.N + 127) / 128, mt);
             switch (g.epi) {

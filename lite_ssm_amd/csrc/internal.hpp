@@ -165,8 +165,18 @@ struct GemmArgs {
     uint32_t M, N, K;
     int wfmt, act, epi;
     int round_dequant;   // gemm_simple only: 1 = GEMM semantics, 0 = exact (GEMV)
+    // prefill GEMM, optional: fp32 workspace of ws_floats floats; a grid of
+    // few tiles then splits K into slices whose sums a second launch adds
+    float* ws = nullptr;
+    size_t ws_floats = 0;
 };
 hipError_t launch_gemm(hipStream_t s, const GemmArgs& a);
+// Workspace the engine gives launch_gemm for its split-K slices (floats).
+// The 130M prefill of 2048 tokens (config 3) runs its out_proj in four slices
+// plus the sum: 2.60 -> 2.45 ms for the whole prefill; the same GEMM alone
+// through lssm_linear (no workspace) measures 23.9 us unsplit against 26.5 us
+// split, so the generic entry keeps the single launch.
+constexpr size_t GEMM_WS_FLOATS = (size_t)8 << 20;   // 32 MiB
 // Simple fp32 (or any dtype) reference-layout GEMM used for F32 activations.
 hipError_t launch_gemm_simple(hipStream_t s, const GemmArgs& a);
 
