@@ -855,6 +855,34 @@ __global__ __launch_bounds__(256) void gemm_split_sum_kernel(GemmArgs a, uint32_
     ((T*)a.y)[yi] = from_f<T>(v);
 }
 
+// The same, four consecutive outputs a thread (N and the row strides
+// multiples of 4): 16-byte loads of the slices' sums.
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void gemm_split_sum4_kernel(GemmArgs a, uint32_t S) {
+    const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x, MN = (size_t)a.M * a.N;
+    if (4 * q >= MN) return;
+    floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t z = 0; z < S; ++z) {
+        const floatx4 p = reinterpret_cast<const floatx4*>(a.ws + z * MN)[q];
+        v[0] += p[0];
+        v[1] += p[1];
+        v[2] += p[2];
+        v[3] += p[3];
+    }
+    const uint32_t m = (uint32_t)(4 * q / a.N), n = (uint32_t)(4 * q % a.N);
+    const size_t yi = (size_t)m * a.y_stride + n;
+    T o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float x = v[e];
+        if (EPI == LSSM_EPI_SILU) x = silu_f(x);
+        if (EPI == LSSM_EPI_ADD) x = to_f(((const T*)a.res)[yi + e]) + rnd<T>(x);
+        o[e] = from_f<T>(x);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ((T*)a.y)[yi + e] = o[e];
+}
+
 // K slices for a prefill GEMM whose 256 x 128 tiles would leave most CUs idle
 // (the 130M out_proj at 2048 rows: 48 tiles): as many as fill about half the
 // CUs, K / 64 divisible, the workspace large enough; 1 = no split.
@@ -914,6 +942,15 @@ hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
             gemm2_kernel<FMT, T, LSSM_EPI_NONE, 4><<<grid, 512, 0, s>>>(a);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
+            if (a.N % 4 == 0 && (uintptr_t)a.ws % 16 == 0) {
+                const unsigned nb = (unsigned)(((size_t)a.M * a.N / 4 + 255) / 256);
+                switch (a.epi) {
+                    case LSSM_EPI_SILU: gemm_split_sum4_kernel<T, LSSM_EPI_SILU><<<nb, 256, 0, s>>>(a, S); break;
+                    case LSSM_EPI_ADD: gemm_split_sum4_kernel<T, LSSM_EPI_ADD><<<nb, 256, 0, s>>>(a, S); break;
+                    default: gemm_split_sum4_kernel<T, LSSM_EPI_NONE><<<nb, 256, 0, s>>>(a, S); break;
+                }
+                return hipGetLastError();
+            }
             const unsigned nb = (unsigned)(((size_t)a.M * a.N + 255) / 256);
             switch (a.epi) {
                 case LSSM_EPI_SILU: gemm_split_sum_kernel<T, LSSM_EPI_SILU><<<nb, 256, 0, s>>>(a, S); break;
