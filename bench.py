@@ -24,7 +24,7 @@ weight copies so every launch reads HBM) and GEMM (M = 2048); 3 = the 130M
 model (prefill 2048, greedy decode); 5 = the 8B model (prefill 8192, decode at
 batch 32).
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip 1,2,3,5,cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip 1,2,3,ref,5,cpu]
 """
 import argparse
 import hashlib
@@ -235,6 +235,52 @@ def bench_linears_130m(L, torch, ctx, timer):
     return out
 
 
+def bench_ref_api(L, torch, ctx, timer, n_new=33, prompt_len=64):
+    """The drop-in path: the reference's own host code (SSMFile, Mamba2Model,
+    generate(); tests/cpp/_bin/ref_model_run, built from the reference sources
+    against include/lite_ssm/*.hpp) on this backend, greedy decode of a
+    130M-shaped int4-b32 / fp16 file, the reference's formats.  Its activations
+    and state live in DeviceBuffers of pinned host memory, so every kernel reaches
+    them over PCIe and every op is a host round trip.  Beside it, the engine on
+    the same file (HBM-resident, one graph launch per four steps).  None when the
+    harness was not built (it needs the reference checkout at build time)."""
+    import subprocess
+    import tempfile
+    from lite_ssm_amd import ssm as S
+    from lite_ssm_amd.model import Engine, shape
+    exe = os.path.join(ROOT, "tests", "cpp", "_bin", "ref_model_run")
+    if not os.path.exists(exe):
+        return None
+    sh = shape("mamba2-130m")
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "m.ssm")
+        S.write_random(path, sh, L.F16, L.W_Q4_B32, seed=1)
+        ids = [(7 * i + 3) % sh.vocab_size for i in range(prompt_len)]
+        r = subprocess.run([exe, path, str(n_new), os.path.join(d, "l.bin"), ",".join(map(str, ids))],
+                           capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            log(f"ref_model_run failed ({r.returncode}): {r.stderr.strip()[-200:]}")
+            return None
+        rec = json.loads(r.stdout.strip().splitlines()[-1])
+        with S.SSMFile(path) as f:
+            fm = f.model(ctx)
+            eng = Engine(ctx, fm, 1, max(prompt_len, sh.chunk_size))
+            try:
+                tb = torch.tensor([ids], dtype=torch.int32, device="cuda")
+                nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+                t_pre = timer(lambda: eng.prefill(tb, nxt))
+                eng.decode_graph(nxt, nxt, 4)
+                t_dec = timer(lambda: eng.decode_graph(nxt, nxt, n_new - 1)) / (n_new - 1)
+            finally:
+                eng.close()
+    return {"workload": "mamba2-130m-shaped, int4-b32 weights, fp16 act, random init; "
+                        f"{prompt_len}-token prompt, {n_new - 1} greedy decode steps at batch 1",
+            "ref_api_prefill_ms": round(rec["first_ms"], 3),
+            "ref_api_decode_tok_s": round((n_new - 1) * 1000.0 / rec["decode_ms"], 1),
+            "engine_prefill_ms": round(t_pre * 1e3, 3),
+            "engine_decode_tok_s": round(1.0 / t_dec, 1)}
+
+
 def bench_model(L, torch, ctx, timer, name, act, wfmt, prefill_batch, prefill_len, decode_batch, steps,
                 seed):
     """A whole random-init model: prefill tokens/s and greedy decode tokens/s."""
@@ -388,7 +434,7 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=3)
     ap.add_argument("--batches", default="4,16", help="extra decode batch sizes to report")
     ap.add_argument("--cpu-steps", type=int, default=8)
-    ap.add_argument("--skip", default="", help="comma list of sections to skip: 1,2,3,5,cpu")
+    ap.add_argument("--skip", default="", help="comma list of sections to skip: 1,2,3,ref,5,cpu")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only run the dominant decode kernel over all layers plus a 256 MiB "
@@ -519,6 +565,12 @@ def main():
         configs["3_130m_q8_f16"] = bench_model(L, torch, ctx, timer, "mamba2-130m", L.F16, L.W_Q8_G32,
                                                1, 2048, 1, 256, 3)
         log(f"config 3: {configs['3_130m_q8_f16']['decode_tok_s']} tok/s decode")
+    if "ref" not in skip:
+        rec = bench_ref_api(L, torch, ctx, timer)
+        if rec is not None:
+            configs["ref_api_130m_q4b32_f16"] = rec
+            log(f"reference API path: {rec['ref_api_decode_tok_s']} tok/s decode "
+                f"(engine {rec['engine_decode_tok_s']})")
     if "5" not in skip:
         configs["5_8b_q4_bf16"] = bench_model(L, torch, ctx, timer, "mamba2-8b", L.BF16, L.W_Q4_G64,
                                               1, 8192, 32, 64, 5)

@@ -6,8 +6,12 @@
 // Usage: ref_model_run <model.ssm> <n_new> <logits.bin> <id,id,...>
 // Greedy-generates n_new tokens after the prompt exactly as the reference's
 // runtime does (src/runtime/inference.cpp:14-70), prints one JSON line
-// {"ids": [...]} and writes the fp32 logits each id was picked from
-// ([n_new, vocab] float32, Mamba2Model::read_logits_fp32) to logits.bin.
+// {"ids": [...], "first_ms": ..., "decode_ms": ...} and writes the fp32 logits
+// each id was picked from ([n_new, vocab] float32,
+// Mamba2Model::read_logits_fp32) to logits.bin.  first_ms is the time from
+// the start of generate() to the first pick (prefill and logits), decode_ms
+// the time from the first pick to the last (n_new - 1 decode steps), both
+// without the logits file writes.
 // Exit 77 (skip) when no GPU is available.
 
 #include "lite_ssm/inference.hpp"
@@ -15,6 +19,7 @@
 #include "lite_ssm/ops.hpp"
 #include "lite_ssm/state.hpp"
 
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <exception>
@@ -54,14 +59,22 @@ int main(int argc, char** argv) {
         gc.greedy = true;
         // the callback runs right after each pick, while the workspace's fp32
         // scratch still holds the logits the id was taken from
+        using clk = std::chrono::steady_clock;
+        double first_ms = 0.0, decode_ms = 0.0, io_ms = 0.0;
+        const auto t0 = clk::now();
         auto ids = lite_ssm::generate(model, ops, ws, state, prompt, gc, [&](uint32_t) {
+            const auto t = clk::now();
+            const double at = std::chrono::duration<double, std::milli>(t - t0).count() - io_ms;
+            if (first_ms == 0.0) first_ms = at;
+            else decode_ms = at - first_ms;
             const std::vector<float>& lg = model.read_logits_fp32(ws);
             std::fwrite(lg.data(), sizeof(float), lg.size(), out);
+            io_ms += std::chrono::duration<double, std::milli>(clk::now() - t).count();
         });
         std::fclose(out);
         std::printf("{\"ids\": [");
         for (size_t i = 0; i < ids.size(); ++i) std::printf("%s%u", i ? ", " : "", ids[i]);
-        std::printf("]}\n");
+        std::printf("], \"first_ms\": %.3f, \"decode_ms\": %.3f}\n", first_ms, decode_ms);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "error: %s\n", e.what());
         return 1;
