@@ -121,7 +121,11 @@ int lssm_sync(lssm_ctx* ctx);              /* stream sync + error check         
  *     LSSM_EINVAL, "Mamba2Model::embed: token_id out of range";
  *   - a bounded cross-workgroup wait of a fused decode launch gave up (its
  *     workgroups were not all resident at once): LSSM_EDEVICE; the affected
- *     outputs are NaN and their SSD state is left as it was.
+ *     outputs are NaN and their SSD state is left as it was, but the conv
+ *     state has advanced by the step's token (the window shift happens in the
+ *     in_proj epilogue, before any wait), so the step must not be retried on
+ *     the same state.
+ *   Both conditions in one step report LSSM_EINVAL with both texts.
  *
  * Failure-injection switches for the tests of these paths (no counterpart in
  * the reference; 0 = off, the default).  LSSM_DEBUG_STALE_WAIT makes the SSD
@@ -426,6 +430,14 @@ int lssm_engine_logits(lssm_engine* e, void** logits);          /* [max_batch, v
  * refused (LSSM_EINVAL).  buf = NULL turns it off.  Not combinable with
  * lssm_engine_decode_graph. */
 int lssm_engine_set_trace(lssm_engine* e, void* buf, uint64_t bytes);
+/* Greedy-id history, the counterpart of the id vector generate() returns
+ * (runtime/inference.cpp:55-67).  With `buf` set, every later decode step
+ * (lssm_engine_decode and each step replayed by lssm_engine_decode_graph)
+ * appends its `batch` greedy ids as the next row of `buf` (device int32
+ * [cap_steps][batch]); steps past cap_steps are not stored.  Setting it
+ * restarts at row 0 and drops captured decode graphs; buf = NULL turns it
+ * off.  Off by default: it adds one small kernel per step. */
+int lssm_engine_set_id_log(lssm_engine* e, int32_t* buf, uint32_t cap_steps);
 int lssm_engine_state(lssm_engine* e, void** conv_state, void** ssd_state);
 /* conv_state: [n_layer, max_batch, xBC_dim, d_conv] act; ssd: [n_layer, max_batch, H, P, N] f32 */
 /* Layers of the last decode step (eager or captured) whose SSD step ran inside

@@ -174,6 +174,7 @@ _SIGS = {
     "lssm_engine_decode_graph": ([_vp, _vp, _u32, _vp, _u32], _i),
     "lssm_engine_logits": ([_vp, C.POINTER(_vp)], _i),
     "lssm_engine_set_trace": ([_vp, _vp, C.c_uint64], _i),
+    "lssm_engine_set_id_log": ([_vp, _vp, _u32], _i),
     "lssm_engine_state": ([_vp, C.POINTER(_vp), C.POINTER(_vp)], _i),
     "lssm_engine_fused_layers": ([_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)], _i),
     # .ssm files

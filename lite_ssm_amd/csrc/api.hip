@@ -5,6 +5,7 @@
 // generic entries with fp16 activations and batch 1.  Every entry validates
 // shapes and alignment on the host before launching, so that no kernel is
 // launched on a shape it does not support.
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 
@@ -231,7 +232,10 @@ int lssm_ssd_chunked(lssm_ctx* ctx, const void* X, const void* B, const void* C,
     // The context's workspaces: the segment workspace (allocated on first
     // use) and the Gram tiles of the MFMA scan (grown on demand).  Neither is
     // allocated while the stream is being captured; the scan then runs
-    // without them (unsegmented, each head forming its own C B^T).
+    // without the ones that do not exist yet (unsegmented, or each head
+    // forming its own C B^T).  A captured launch may keep either address, so
+    // neither is freed before lssm_ctx_destroy: a grown-out Gram buffer is
+    // retired, not freed.
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     hipError_t e = hipStreamIsCapturing(ctx->stream, &cap);
     if (e != hipSuccess) return set_error(LSSM_EDEVICE, "ssd_chunked: %s", hipGetErrorString(e));
@@ -245,20 +249,14 @@ int lssm_ssd_chunked(lssm_ctx* ctx, const void* X, const void* B, const void* C,
         }
         const size_t gf = ssd_gram_floats(batch, d.L, d.n_groups);
         if (act != LSSM_F32 && ctx->ssd_gram_cap < gf) {
-            if (ctx->ssd_gram) {
-                // the old tiles may still be read by launches in flight
-                e = hipStreamSynchronize(ctx->stream);
-                if (e == hipSuccess) e = hipFree(ctx->ssd_gram);
-                ctx->ssd_gram = nullptr;
-                ctx->ssd_gram_cap = 0;
-                if (e != hipSuccess) return set_error(LSSM_EDEVICE, "ssd_chunked: %s", hipGetErrorString(e));
-            }
-            e = hipMalloc((void**)&ctx->ssd_gram, gf * sizeof(float));
-            if (e != hipSuccess) {
-                ctx->ssd_gram = nullptr;
+            const size_t want = std::max(gf, 2 * ctx->ssd_gram_cap);
+            float* p = nullptr;
+            e = hipMalloc((void**)&p, want * sizeof(float));
+            if (e != hipSuccess)
                 return set_error(LSSM_EDEVICE, "ssd_chunked: Gram workspace: %s", hipGetErrorString(e));
-            }
-            ctx->ssd_gram_cap = gf;
+            if (ctx->ssd_gram) ctx->ssd_gram_retired.push_back(ctx->ssd_gram);
+            ctx->ssd_gram = p;
+            ctx->ssd_gram_cap = want;
         }
     }
     a.seg = ctx->ssd_seg;

@@ -41,13 +41,20 @@ int sync_and_check(lssm_ctx* ctx, const char* what) {
     e = hipMemcpyAsync(ctx->status, ctx->status_host, sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return set_error(LSSM_EDEVICE, "%s failed: %s", what, hipGetErrorString(e));
+    // The fused decode launch shifts each conv window in its in_proj epilogue,
+    // before any SSD item waits, so a timed-out step has advanced the conv
+    // state by its token while leaving the waiting items' SSD state alone.
+    const char* wait_msg =
+        "a cross-workgroup wait timed out (the launch's workgroups were not all resident at once); "
+        "the affected outputs are NaN and their SSD state was not updated, but the conv state did "
+        "advance by this step's token";
     // mamba2_model.cpp:129-131 throws std::out_of_range with this text
+    if ((st & STATUS_BAD_TOKEN) && (st & STATUS_WAIT_TIMEOUT))
+        return set_error(LSSM_EINVAL, "Mamba2Model::embed: token_id out of range (%s); also: %s", what,
+                         wait_msg);
     if (st & STATUS_BAD_TOKEN)
         return set_error(LSSM_EINVAL, "Mamba2Model::embed: token_id out of range (%s)", what);
-    return set_error(LSSM_EDEVICE,
-                     "%s: a cross-workgroup wait timed out (the launch's workgroups were not all "
-                     "resident at once); the affected outputs are NaN and their state was not updated",
-                     what);
+    return set_error(LSSM_EDEVICE, "%s: %s", what, wait_msg);
 }
 
 int finish(lssm_ctx* ctx, const char* what) {
@@ -127,6 +134,7 @@ int lssm_ctx_destroy(lssm_ctx* ctx) {
     (void)hipHostFree(ctx->status_host);
     if (ctx->ssd_seg) (void)hipFree(ctx->ssd_seg);
     if (ctx->ssd_gram) (void)hipFree(ctx->ssd_gram);
+    for (float* p : ctx->ssd_gram_retired) (void)hipFree(p);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return LSSM_OK;

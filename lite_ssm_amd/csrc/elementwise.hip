@@ -437,6 +437,20 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* pv, cons
     if (threadIdx.x == 0) ids[row] = (bi == 0x7fffffff) ? 0 : bi;
 }
 
+// Greedy-id history of a decode run (runtime/inference.cpp:55-67 collects the
+// generated ids into a vector): row `*pos` of log [cap][B] gets this step's
+// ids, then *pos advances.  Every thread reads *pos before the barrier and
+// thread 0 writes it after, so the block sees one value.  Steps past `cap`
+// are counted and not stored.
+__global__ __launch_bounds__(64) void id_log_kernel(const int32_t* __restrict__ next, uint32_t B,
+                                                    int32_t* __restrict__ log, uint32_t cap,
+                                                    uint32_t* __restrict__ pos) {
+    const uint32_t p = *pos;
+    __syncthreads();
+    if (threadIdx.x < B && p < cap) log[(size_t)p * B + threadIdx.x] = next[threadIdx.x];
+    if (threadIdx.x == 0) *pos = p + 1u;
+}
+
 static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 // Chunks of 512 elements per row for the wave-per-row norms (0 = use the
@@ -636,6 +650,13 @@ hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32
                       argmax_partial_kernel<T, 256><<<dim3(nblk, rows), 256, 0, s>>>(
                           (const T*)logits, vocab, pv, pi, ids));
     argmax_final_kernel<<<rows, 256, 0, s>>>(pv, pi, nblk, ids);
+    return hipGetLastError();
+}
+
+hipError_t launch_id_log(hipStream_t s, const int32_t* next, uint32_t B, int32_t* log, uint32_t cap,
+                         uint32_t* pos) {
+    if (B == 0 || B > 64) return hipErrorInvalidValue;
+    id_log_kernel<<<1, 64, 0, s>>>(next, B, log, cap, pos);
     return hipGetLastError();
 }
 

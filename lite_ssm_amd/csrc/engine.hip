@@ -119,6 +119,10 @@ struct lssm_engine {
     // and after the last one, [n_layer + 1][rows][d_model], or null
     void* trace = nullptr;
     size_t trace_cap = 0;
+    // greedy-id history (lssm_engine_set_id_log): every decode step, eager or
+    // graph-replayed, appends its ids as row seq[1] of id_log [id_log_cap][batch]
+    int32_t* id_log = nullptr;
+    uint32_t id_log_cap = 0;
     size_t trace_bytes(uint32_t rows) const { return (size_t)(cfg.n_layer + 1) * rows * d_model * es; }
     hipError_t trace_rows(uint32_t slot, const void* h, uint32_t rows) const {
         if (!trace) return hipSuccess;
@@ -348,6 +352,7 @@ struct lssm_engine {
         }
         if (e == hipSuccess) e = trace_rows(cfg.n_layer, d_hidden, B);
         if (e == hipSuccess) e = logits_argmax(d_hidden, d_model, B, next);
+        if (e == hipSuccess && id_log) e = launch_id_log(st(), next, B, id_log, id_log_cap, seq + 1);
         return e;
     }
 
@@ -664,6 +669,16 @@ int lssm_engine_set_trace(lssm_engine* e, void* buf, uint64_t bytes) {
     e->trace = buf;
     e->trace_cap = buf ? (size_t)bytes : 0;
     return LSSM_OK;
+}
+
+int lssm_engine_set_id_log(lssm_engine* e, int32_t* buf, uint32_t cap_steps) {
+    if (int rc = check_engine(e)) return rc;
+    LSSM_REQUIRE(!buf || cap_steps > 0, "engine_set_id_log: empty buffer");
+    e->drop_graphs();                       // captured steps hold the old setting
+    e->id_log = buf;
+    e->id_log_cap = buf ? cap_steps : 0;
+    return engine_finish(e, hipMemsetAsync(e->seq + 1, 0, sizeof(uint32_t), e->ctx->stream),
+                         "engine_set_id_log");
 }
 
 int lssm_engine_decode_graph(lssm_engine* e, const int32_t* ids, uint32_t batch, int32_t* next_ids,

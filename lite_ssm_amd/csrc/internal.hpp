@@ -12,6 +12,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "../../include/lssm.h"
 
@@ -30,8 +31,11 @@ struct lssm_ctx {
     // allocated by the first lssm_ssd_chunked call that can use it
     float* ssd_seg = nullptr;
     // Gram tiles of lssm_ssd_chunked (lssm::ssd_gram_floats), grown on demand
+    // to at least twice the last size.  A grown-out buffer is kept until
+    // lssm_ctx_destroy: a graph captured on this stream may hold its address.
     float* ssd_gram = nullptr;
     size_t ssd_gram_cap = 0;   // floats
+    std::vector<float*> ssd_gram_retired;
 };
 
 namespace lssm {
@@ -113,6 +117,9 @@ hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, vo
                         uint32_t* seq = nullptr);
 hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32_t rows,
                          uint32_t vocab, int act, void* scratch);
+// appends next[0..B) as row *pos of log [cap][B] and advances *pos (B <= 64)
+hipError_t launch_id_log(hipStream_t s, const int32_t* next, uint32_t B, int32_t* log, uint32_t cap,
+                         uint32_t* pos);
 
 // GEMV (M <= 4): optional RMSNorm prologue over each x row (norm_w != nullptr).
 struct GemvArgs {

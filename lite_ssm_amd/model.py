@@ -114,10 +114,17 @@ class DeviceModel:
     """Random-init Mamba-2 weights resident in HBM (one GPU)."""
 
     def __init__(self, sh: Shape, act: int = BF16, wfmt: int = W_Q4_G64, seed: int = 0,
-                 device: str = "cuda", std: float = 0.02, embed_std: float | None = None):
+                 device: str = "cuda", std: float = 0.02, embed_std: float | None = None,
+                 head: str = "tied"):
         """Random init: linears ~ N(0, std), embeddings ~ N(0, embed_std or std).
-        A larger embed_std (the lm_head is tied) spreads the logits, so the
-        greedy choice is rarely a near-tie at the logits' fp16 resolution."""
+
+        head = "tied": lm_head is the embedding (mamba2_model.cpp:75-83).
+        head = "permuted": lm_head row pi(j) is embedding row j, for a random
+        permutation pi.  With a large embed_std the residual stream keeps the
+        input token's embedding, so a tied head mostly predicts the input token
+        again (greedy decoding repeats one id); the permuted head predicts
+        pi(input) instead, and greedy decoding walks a long cycle of pi, with
+        top-2 margins that the layers' outputs move but rarely close."""
         self.shape, self.act, self.wfmt, self.device = sh, act, wfmt, device
         dt = TORCH_DTYPE[act]
         g = torch.Generator(device=device)
@@ -155,7 +162,14 @@ class DeviceModel:
             Lw["mixer_norm_w"] = act_t(randn(sh.d_inner, scale=0.1, mean=1.0))
             Lw["out_proj_w"], Lw["out_proj_s"] = lin(sh.d_model, sh.d_inner)
             self.layers.append(Lw)
-        self.lm_head = self.embed   # tied (mamba2_model.cpp:75-83)
+        if head == "tied":
+            self.lm_head = self.embed   # tied (mamba2_model.cpp:75-83)
+        elif head == "permuted":
+            perm = torch.randperm(sh.vocab_size, generator=g, device=device)
+            self.lm_head = torch.empty_like(self.embed)
+            self.lm_head[perm] = self.embed
+        else:
+            raise ValueError(f"head must be 'tied' or 'permuted', not {head!r}")
 
     # -- C-ABI views ------------------------------------------------------
     def config(self) -> ModelConfig:
@@ -259,6 +273,16 @@ class Engine:
         else:
             check(lib.lssm_engine_set_trace(self.h, buf.data_ptr(), buf.numel() * buf.element_size()))
         self._trace = buf
+
+    def set_id_log(self, buf):
+        """Every later decode step (eager or graph-replayed) appends its greedy
+        ids to `buf` (device int32 [steps, batch]) row by row; None turns it off."""
+        if buf is None:
+            check(lib.lssm_engine_set_id_log(self.h, None, 0))
+        else:
+            assert buf.dtype == torch.int32 and buf.is_contiguous()
+            check(lib.lssm_engine_set_id_log(self.h, buf.data_ptr(), buf.shape[0]))
+        self._id_log = buf
 
     def fused_layers(self):
         """(layers of the last decode step whose SSD step ran inside the in_proj

@@ -97,6 +97,8 @@ _SIGS = {
     "orc_model_logits": ([C.POINTER(_Model), _vp, _u32, _vp], None),
     "orc_num_threads": ([], _i),
     "orc_set_num_threads": ([_i], None),
+    "orc_set_accum": ([_i], None),
+    "orc_accum": ([], _i),
 }
 for _n, (_a, _r) in _SIGS.items():
     _fn = getattr(_L, _n)
@@ -343,3 +345,20 @@ def num_threads():
 
 def set_num_threads(n):
     _L.orc_set_num_threads(int(n))
+
+
+def set_accum(f32):
+    """Summation of the linears' dot products: False = double (default),
+    True = float32 in sixteen partial sums (see lssm_oracle.c)."""
+    _L.orc_set_accum(1 if f32 else 0)
+
+
+class accum_f32:
+    """with O.accum_f32(): ... runs the oracle with float32 sums."""
+
+    def __enter__(self):
+        self._old = int(_L.orc_accum())
+        _L.orc_set_accum(1)
+
+    def __exit__(self, *exc):
+        _L.orc_set_accum(self._old)

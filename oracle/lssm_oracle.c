@@ -133,6 +133,16 @@ void orc_set_num_threads(int n) {
 #endif
 }
 
+/* Summation of the linears' dot products: double (the default, as close to
+ * exact as the oracle gets) or float32 in sixteen interleaved partial sums.
+ * The reference's kernels accumulate in fp32 in their own order
+ * (linear.metal:100-108, 463-473), so both are faithful restatements; the
+ * float32 mode exists to measure how far two such restatements part over a
+ * whole model, which is the yardstick for the GPU path's whole-model drift. */
+static int g_accum_f32 = 0;
+void orc_set_accum(int f32) { g_accum_f32 = f32 != 0; }
+int orc_accum(void) { return g_accum_f32; }
+
 /* ------------------------------------------------------------------------- */
 /* weight formats                                                             */
 /* ------------------------------------------------------------------------- */
@@ -295,6 +305,19 @@ static void dot4_f64(const double* w, const double* x, uint32_t K, double* out) 
     }
 }
 
+/* float32 sums of w[k] * x[k], sixteen partial sums added pairwise */
+static float dot1_f32(const double* w, const double* x, uint32_t K) {
+    float p[16] = {0};
+    uint32_t k = 0;
+    for (; k + 16 <= K; k += 16)
+        for (int j = 0; j < 16; ++j) p[j] = fmaf((float)w[k + j], (float)x[k + j], p[j]);
+    for (int w2 = 8; w2 >= 1; w2 >>= 1)
+        for (int j = 0; j < w2; ++j) p[j] += p[j + w2];
+    float t = p[0];
+    for (; k < K; ++k) t = fmaf((float)w[k], (float)x[k], t);
+    return t;
+}
+
 static double dot1_f64(const double* w, const double* x, uint32_t K) {
     v4d a = {0, 0, 0, 0}, b = a, c = a, d = a;
     uint32_t k = 0;
@@ -333,7 +356,8 @@ void orc_linear(const void* x, uint32_t x_stride, const void* w, const void* s, 
             for (uint32_t k = 0; k < K; ++k) wd[k] = wr[k];
             double dots[4];
             for (uint32_t m = 0; m < M; ++m) {
-                if (m % 4 == 0 && M - m >= 4) dot4_f64(wd, xd + (size_t)m * K, K, dots);
+                if (g_accum_f32) dots[m % 4] = dot1_f32(wd, xd + (size_t)m * K, K);
+                else if (m % 4 == 0 && M - m >= 4) dot4_f64(wd, xd + (size_t)m * K, K, dots);
                 else if (M - (m - m % 4) < 4) dots[m % 4] = dot1_f64(wd, xd + (size_t)m * K, K);
                 float a = (float)dots[m % 4];
                 size_t yi = (size_t)m * y_stride + (size_t)n;

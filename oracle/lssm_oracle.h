@@ -106,6 +106,9 @@ void orc_model_logits(const orc_model* m, const void* rows_h, uint32_t rows, voi
 
 int orc_num_threads(void);
 void orc_set_num_threads(int n);
+/* summation of the linears: 0 = double (default), 1 = float32 */
+void orc_set_accum(int f32);
+int orc_accum(void);
 
 #ifdef __cplusplus
 }

@@ -9,8 +9,37 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 
+# Parity figures that tests report (identical-id prefixes, worst errors over
+# long decodes): printed in the terminal summary, which `pytest -q` keeps, and
+# written as JSON lines to $LSSM_PARITY_RECORD when that is set.
+RECORDS = []
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not RECORDS:
+        return
+    import json
+    terminalreporter.write_sep("-", "parity records")
+    for r in RECORDS:
+        terminalreporter.write_line(json.dumps(r, sort_keys=True, default=float))
+    path = os.environ.get("LSSM_PARITY_RECORD")
+    if path:
+        with open(path, "a") as f:
+            for r in RECORDS:
+                f.write(json.dumps(r, sort_keys=True, default=float) + "\n")
+
+
+@pytest.fixture
+def parity_record():
+    """record(name, **figures): keep a test's parity figures for the summary."""
+    def record(name, **fig):
+        RECORDS.append(dict(test=name, **fig))
+        print(f"[parity] {name}: {fig}", flush=True)
+    return record
 
 
 @pytest.fixture(scope="session")

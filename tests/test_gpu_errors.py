@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import act_host, dev, empty
+from gpu_util import act_host, assert_close, dev, empty
 
 pytestmark = pytest.mark.gpu
 
@@ -73,8 +73,9 @@ def test_engine_out_of_range_id_raises(ctx):
 
 def test_fused_decode_wait_timeout_is_reported(ctx, rng):
     """The fused batch-1 in_proj + SSD launch with waits that cannot succeed:
-    LSSM_EDEVICE, the SSD state untouched, the outputs NaN; afterwards the same
-    call without the switch succeeds and matches the separate launches."""
+    LSSM_EDEVICE, the SSD state untouched, the outputs NaN, the conv window
+    shifted by the step's token (as the message says); afterwards the same
+    call without the switch succeeds."""
     L = _lib()
     act, wfmt = O.F16, O.W_Q8_G32
     d_model, d_inner, N, G, H, K = 768, 1536, 128, 1, 24, 4
@@ -102,6 +103,7 @@ def test_fused_decode_wait_timeout_is_reported(ctx, rng):
             cb.data_ptr(), dtb.data_ptr(), alog.data_ptr(), Dh.data_ptr(), st.data_ptr(), y.data_ptr(),
             xfer.data_ptr(), tag, d_model, d_inner, N, G, H, P, K, 1e-5, wfmt, act)
 
+    cs0 = act_host(cs, act).copy()
     ctx.set_debug(L.DEBUG_STALE_WAIT)
     try:
         rc = call(1)
@@ -109,9 +111,15 @@ def test_fused_decode_wait_timeout_is_reported(ctx, rng):
     finally:
         ctx.set_debug(0)
     assert rc == 2, "LSSM_EDEVICE expected"
-    assert "timed out" in msg, msg
+    assert "timed out" in msg and "conv state did advance" in msg, msg
     assert np.array_equal(st.cpu().numpy(), st0), "SSD state must be left as it was"
     assert np.isnan(O.from_act(act_host(y, act), act)).all(), "timed-out outputs are NaN"
+    # the conv window shifted: taps 1..3 moved down, the projection's xBC row in tap 3
+    cs1 = act_host(cs, act)
+    assert np.array_equal(cs1[..., :K - 1], cs0[..., 1:]), "conv window not shifted"
+    normed = O.rmsnorm(act_host(hid, act), act_host(nw, act), 1e-5, act)
+    prow = O.linear(normed, wq, sq, 1, proj, d_model, wfmt, act)
+    assert_close(cs1[0, :, K - 1], prow[0, d_inner:d_inner + xbc], act, 2e-3, "conv tap 3")
     # without the switch: succeeds, state advanced, finite outputs
     L.check(call(2))
     assert not np.array_equal(st.cpu().numpy(), st0)

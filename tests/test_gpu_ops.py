@@ -401,6 +401,59 @@ def test_ssd_chunked_mfma_vs_oracle(ctx, rng, act, batch, Lq, H, G, P):
     assert max_rel(host(sd, np.float32), s2) < 2e-2
 
 
+def test_ssd_chunked_graph_survives_gram_growth(ctx, rng):
+    """A graph captured around lssm_ssd_chunked records the context's Gram
+    workspace; a later, larger uncaptured call grows that workspace.  The old
+    buffer must stay allocated (retired until lssm_ctx_destroy), so every
+    replay of the graph still gives the eager bits."""
+    L = _lib()
+    act, P, N, G = O.BF16, 64, 128, 1
+    st = torch.cuda.Stream()
+    c2 = L.Ctx(st.cuda_stream)
+    try:
+        def inputs(batch, Lq, H):
+            X, B, Cc, dt, dtb, A_log, D = _ssd_inputs(rng, batch, Lq, H, P, N, G, act)
+            return [dev(a) for a in (X, B, Cc, dt, dtb, A_log, D)]
+
+        small = (1, 192, 8)
+        a = inputs(*small)
+        s0 = torch.from_numpy((rng.standard_normal((1, 8, P, N)) * 0.2).astype(np.float32)).cuda()
+        sd = s0.clone()
+        Y = empty((1, 192, 8, P), act)
+        dims = L.SSDDims(192, 8, P, N, G, 64, 1e-6, 1e6, 1)
+        with torch.cuda.stream(st):
+            c2.ssd_chunked(*a, Y, sd, 1, dims, act)          # allocates the workspaces
+        st.synchronize()
+        Ye, se = Y.clone(), sd.clone()
+        g = torch.cuda.CUDAGraph()
+        sd.copy_(s0)
+        Y.zero_()
+        torch.cuda.synchronize()
+        c2.begin_batch()
+        with torch.cuda.stream(st):
+            g.capture_begin()
+            c2.ssd_chunked(*a, Y, sd, 1, dims, act)
+            g.capture_end()
+        c2.commit_and_wait()
+        # a larger call grows the Gram workspace
+        big = inputs(4, 1024, 8)
+        sb = torch.zeros(4, 8, P, N, dtype=torch.float32, device="cuda")
+        Yb = empty((4, 1024, 8, P), act)
+        with torch.cuda.stream(st):
+            c2.ssd_chunked(*big, Yb, sb, 4, L.SSDDims(1024, 8, P, N, G, 64, 1e-6, 1e6, 1), act)
+        st.synchronize()
+        for _ in range(3):
+            sd.copy_(s0)
+            Y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(Y, Ye) and torch.equal(sd, se)
+    finally:
+        torch.cuda.synchronize()
+        c2.close()
+
+
 def test_ssd_chunked_reference_entry_and_checks(ctx, rng):
     L = _lib()
     lib = L.lib

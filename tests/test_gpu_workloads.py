@@ -87,16 +87,18 @@ def test_lm_head_gemv_real_vocab(ctx, N, K, act, rows):
 
 
 # --------------------------------------------------------------------------- config 3
-def test_config3_130m_prefill2048_greedy256(ctx):
+def test_config3_130m_prefill2048_greedy256(ctx, parity_record):
     from lite_ssm_amd.model import DeviceModel, Engine, shape
     print("case: config 3 (130M int8-g32 fp16, prefill 2048, 256 greedy steps)", flush=True)
     act, wfmt = O.F16, O.W_Q8_G32
     sh = shape("mamba2-130m")
-    # embeddings (tied lm_head) ~ N(0, 1): logits spread over tens of units, so
-    # the top-2 margin is rarely below the fp16 resolution of the logits and
-    # free-running ids are a meaningful comparison (with N(0, 0.02) the logits
-    # sit within a few fp16 ulps of each other and ties are common)
-    m = DeviceModel(sh, act=act, wfmt=wfmt, seed=3, embed_std=1.0)
+    # embeddings ~ N(0, 1): logits spread over tens of units, so the top-2
+    # margin is rarely below the fp16 resolution of the logits (with N(0, 0.02)
+    # they sit within a few fp16 ulps of each other and ties are common).  The
+    # head is a permutation of the embedding rows: with a tied head the
+    # residual stream's copy of the input embedding makes the input token the
+    # greedy choice again, and 256 free-running steps repeat one id.
+    m = DeviceModel(sh, act=act, wfmt=wfmt, seed=3, embed_std=1.0, head="permuted")
     om = O.Model(m.to_host(), vars(sh), act, wfmt)
     Lp, steps = 2048, 256
     ids = torch.randint(0, sh.vocab_size, (1, Lp), generator=torch.Generator().manual_seed(33),
@@ -127,25 +129,35 @@ def test_config3_130m_prefill2048_greedy256(ctx):
                 assert int(np.argmax(g)) == ref_ids[t], f"step {t}: greedy id"
             if t + 1 < steps:
                 eng.decode(torch.tensor([ref_ids[t]], dtype=torch.int32, device="cuda"), nxt)
-        # free-running: the engine's own ids through the captured decode graph
+        # free-running: the engine's own ids through the captured decode graphs
+        # (four steps per graph launch, as the bench replays them), recorded
+        # on the device by the id log
         eng.reset()
         tok = torch.zeros(1, dtype=torch.int32, device="cuda")
         eng.prefill(ids.cuda(), tok)
-        gpu_ids = [int(tok.item())]
-        for t in range(1, steps):
-            eng.decode_graph(tok, tok, 1)
-            gpu_ids.append(int(tok.item()))
+        id0 = int(tok.item())
+        log = torch.full((steps - 1, 1), -1, dtype=torch.int32, device="cuda")
+        eng.set_id_log(log)
+        eng.decode_graph(tok, tok, steps - 1)
+        eng.set_id_log(None)
+        gpu_ids = [id0] + [int(v) for v in log[:, 0].cpu()]
     finally:
         eng.close()
     same = next((t for t in range(steps) if gpu_ids[t] != ref_ids[t]), steps)
     near = sum(1 for mg, ea in zip(margins, errabs) if mg <= 2 * ea)
+    distinct = len(set(gpu_ids))
     print(f"config 3: identical greedy prefix {same}/{steps}; teacher-forced logits max-rel "
           f"max {max(errs):.2e}; smallest top-2 margin {min(margins):.3e}; "
-          f"steps with a margin within twice the error: {near}", flush=True)
+          f"steps with a margin within twice the error: {near}; distinct ids {distinct}", flush=True)
+    parity_record("config 3 130M free-running 256 (4-step graphs)", identical_prefix=f"{same}/{steps}",
+                  distinct_ids=distinct, logits_maxrel_worst=round(max(errs), 6),
+                  smallest_top2_margin=round(min(margins), 4), near_tie_steps=near)
     if same < steps:
         # the first divergence must be a near-tie the observed error can flip
         assert margins[same] <= 2 * errabs[same], \
             f"free-running ids diverge at step {same} with a clear margin {margins[same]:.3e}"
+    assert same >= 200, f"identical greedy prefix only {same}/{steps}"
+    assert distinct >= 32, f"the free-running ids repeat: {distinct} distinct in {steps}"
 
 
 # --------------------------------------------------------------------------- configs 4 / 5, layer by layer

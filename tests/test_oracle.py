@@ -149,6 +149,39 @@ def test_linear_vs_fp64(rng, act, wfmt):
     assert np.allclose(ya, ref_add, rtol=2 ** -7, atol=1e-6)
 
 
+def test_linear_float32_sums_mode(rng):
+    """O.accum_f32(): the linears sum in float32 (sixteen partial sums) instead
+    of double.  Pinned against fp64: within the float32 summation bound
+    (K + 16) * 2^-24 * sum |w x| of the exact product, not bit-equal to the
+    double mode somewhere at K = 5120 (a different order really runs), bf16
+    outputs equal to the double mode's wherever the exact value is not within
+    that bound of a bf16 rounding boundary, and the default restored on exit."""
+    M, N, K = 4, 256, 5120
+    x = (rng.standard_normal((M, K))).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    bound = (K + 16) * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    y64 = O.linear(x, w, None, M, N, K, O.W_DENSE, O.F32)
+    with O.accum_f32():
+        y32 = O.linear(x, w, None, M, N, K, O.W_DENSE, O.F32)
+    assert np.all(np.abs(y64 - exact) <= np.abs(exact) * 2.0 ** -24 + 1e-30)
+    assert np.all(np.abs(y32 - exact) <= bound)
+    assert not np.array_equal(y32, y64)
+    # back to double sums after the block
+    assert np.array_equal(O.linear(x, w, None, M, N, K, O.W_DENSE, O.F32), y64)
+    # bf16 outputs: the two modes round to the same value unless the exact sum
+    # lies within the float32 bound of a rounding boundary
+    xb, wb = O.to_act(x, O.BF16), O.to_act(w, O.BF16)
+    exb = O.from_act(xb, O.BF16).astype(np.float64) @ O.from_act(wb, O.BF16).astype(np.float64).T
+    b64 = O.from_act(O.linear(xb, wb, None, M, N, K, O.W_DENSE, O.BF16), O.BF16)
+    with O.accum_f32():
+        b32 = O.from_act(O.linear(xb, wb, None, M, N, K, O.W_DENSE, O.BF16), O.BF16)
+    lo = O.round_act((exb - bound).astype(np.float32), O.BF16)
+    hi = O.round_act((exb + bound).astype(np.float32), O.BF16)
+    clear = lo == hi
+    assert np.array_equal(b32[clear], b64[clear])
+
+
 # --------------------------------------------------------------------------- norms / activations
 @pytest.mark.parametrize("act", ACTS)
 def test_rmsnorm_vs_fp64(rng, act):
