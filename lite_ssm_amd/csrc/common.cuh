@@ -79,6 +79,35 @@ __device__ __forceinline__ float swap_add32(float v) {           // lane halves
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave, in a fixed order: within
+// each 16-lane row by DPP row shifts (1, 2, 4, 8), then across rows by the
+// row broadcasts of lanes 15 (into rows 1 and 3) and 31 (into rows 2 and 3).
+// Lanes and rows without a source add 0.
+template <int CTRL, int ROWS> __device__ __forceinline__ float dpp_rows0(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, true));
+}
+__device__ __forceinline__ float wave_prefix_sum(float v) {
+    v += dpp_rows0<0x111, 0xF>(v);   // row_shr:1
+    v += dpp_rows0<0x112, 0xF>(v);   // row_shr:2
+    v += dpp_rows0<0x114, 0xF>(v);   // row_shr:4
+    v += dpp_rows0<0x118, 0xF>(v);   // row_shr:8
+    v += dpp_rows0<0x142, 0xA>(v);   // row_bcast:15
+    v += dpp_rows0<0x143, 0xC>(v);   // row_bcast:31
+    return v;
+}
+
+// Value of lane `l` (wave-uniform) of v, as bits: the builtin takes an int,
+// and a float argument would be converted by value.
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// softplus with the hardware exp and log (about 1 ulp each; the reference's
+// kernels are built with fast math, CMakeLists.txt:122)
+__device__ __forceinline__ float softplus_fast(float v) {
+    return (v > 20.0f) ? v : __logf(1.0f + __expf(v));
+}
+
 // Sum over aligned groups of `W` lanes (W a power of two <= 64); the result in
 // every lane of the group.
 template <int W> __device__ __forceinline__ float group_sum(float v) {

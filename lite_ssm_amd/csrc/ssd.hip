@@ -277,6 +277,13 @@ __global__ __launch_bounds__(SC_NT) void ssd_chunk_scalar_kernel(SsdArgs a) {
 // and dt are prefetched into registers during the current chunk; two
 // barriers per chunk.
 // ---------------------------------------------------------------------------
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its global loads and stores (a __syncthreads would also
+// wait for the register prefetch of later chunks and for the Y stores).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 constexpr int CQ = 64;            // chunk
 constexpr int CN = 128;           // state size
 constexpr int SPAD = CN + 8;      // B / C row pitch (elements)
@@ -307,11 +314,22 @@ template <typename T> __device__ __forceinline__ short bits_of(float v) {
 template <typename T> __device__ __forceinline__ float val_of(short v) {
     return to_f(__builtin_bit_cast(T, v));
 }
+typedef float f32x2s __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2s __attribute__((ext_vector_type(2)));
+typedef short s2v __attribute__((ext_vector_type(2)));
 template <typename T> __device__ __forceinline__ s4v pack4(floatx4 v) {
-    s4v r;
+    if constexpr (__is_same(T, bf16)) {
+        // two v_cvt_pk_bf16_f32 (round to nearest even, as each value alone)
+        typedef uint32_t u32x2s __attribute__((ext_vector_type(2)));
+        const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2s{v[0], v[1]}, bf16x2s));
+        const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2s{v[2], v[3]}, bf16x2s));
+        return __builtin_bit_cast(s4v, u32x2s{lo, hi});
+    } else {
+        s4v r;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = bits_of<T>(v[e]);
-    return r;
+        for (int e = 0; e < 4; ++e) r[e] = bits_of<T>(v[e]);
+        return r;
+    }
 }
 __device__ __forceinline__ s8v cat8(s4v lo, s4v hi) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -389,6 +407,12 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
     // per-token chunk scalars, double-buffered: wave 0 computes chunk c + 1's
     // while the block works on chunk c
     __shared__ __attribute__((aligned(16))) float LCb[2][CQ], DTb[2][CQ], ELb[2][CQ], Wb[2][CQ];
+    // the masked decay factored per 16-token block T (r = 16 T):
+    // e^{Lc_t - Lc_j} DT_j = AFb[t] * BFb[T][j], AFb[t] = e^{Lc_t - Lc_r} (t in
+    // block T), BFb[T][j] = e^{Lc_r - Lc_j} DT_j (j < r + 16); SFb bit T set when
+    // block T's own decay is small enough for its diagonal tile to use them
+    __shared__ __attribute__((aligned(16))) float AFb[2][CQ], BFb[2][4][CQ];
+    __shared__ uint32_t SFb[2];
     // SPL = 2: each wave's updated state tiles for its partner
     __shared__ __attribute__((aligned(16))) s4v Sx[SPL == 2 ? NWV * NST * 64 : 1];
 
@@ -438,13 +462,21 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) dfr[par][e] = (e == 16 * par + li - 8 * lq) ? bits_of<T>(D_h) : (short)0;
 
-    // ---- register prefetch of one chunk: uniform chunk base + fixed 32-bit
-    // per-thread byte offsets.  Rows past L (last chunk) re-read row t0:
-    // they only meet M entries that are masked and state weights w = 0. ----
+    // ---- register prefetch of one chunk through buffer loads: a resource
+    // per tensor and chunk (base = the chunk's first row, range = its tl
+    // rows), a fixed 32-bit per-thread offset and a uniform offset per row
+    // group, so no per-lane address arithmetic.  Rows past L (last chunk)
+    // fall outside the range and read 0: they only meet M entries that are
+    // masked and state weights w = 0. ----
     const uint32_t brow = tid / 16, bcol = (tid % 16) * 8;
     const uint32_t xrow = tid / (PB / 8), xcol = (tid % (PB / 8)) * 8;
     const uint32_t boff = (brow * a.b_stride + bcol) * sizeof(T), coff = (brow * a.c_stride + bcol) * sizeof(T);
     const uint32_t xoff = (xrow * a.x_stride + xcol) * sizeof(T);
+    const uint32_t bstep = BR * a.b_stride * sizeof(T), cstep = BR * a.c_stride * sizeof(T);
+    const uint32_t xstep = XR * a.x_stride * sizeof(T);
+    auto rsrc = [](const void* p, uint32_t bytes) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+    };
     u32x4 rb[BV], rc[BV], rx[XV];   // (vector types: a struct uint4 copies
                                     // through memory and stays in scratch)
     uint32_t rdt = 0;
@@ -459,39 +491,29 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
     auto fetch = [&](uint32_t t0) {
         const uint32_t tl = min((uint32_t)CQ, L - t0);
         if constexpr (GP) {
-            const float* gc = a.gram + (((size_t)b * nchk + t0 / CQ) * a.G + g) * (CQ * CQ);
+            const auto rg = rsrc(a.gram + (((size_t)b * nchk + t0 / CQ) * a.G + g) * (CQ * CQ), CQ * CQ * 4);
 #pragma unroll
             for (int i = 0; i < NTL; ++i) {
                 const int kt = w + NWV * i;
                 const int jt = (int)(JT >> (4 * kt)) & 15;
                 const int J = jt & 3, Tt = jt >> 2;
                 if (kt < 12 && kt != 0 && kt != 4)
-                    rgn[i] = *reinterpret_cast<const floatx4*>(gc + (size_t)(16 * Tt + li) * CQ + 16 * J + 4 * lq);
+                    rgn[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                        rg, (uint32_t)(((16 * Tt + li) * CQ + 16 * J + 4 * lq) * 4), 0, 0));
             }
         }
-        if (tl == CQ) {
+        const auto rB = rsrc(Bv + (size_t)t0 * a.b_stride, ((tl - 1) * a.b_stride + CN) * sizeof(T));
+        const auto rC = rsrc(Cv + (size_t)t0 * a.c_stride, ((tl - 1) * a.c_stride + CN) * sizeof(T));
+        const auto rX = rsrc(X + (size_t)t0 * a.x_stride, ((tl - 1) * a.x_stride + PB) * sizeof(T));
 #pragma unroll
-            for (int v = 0; v < BV; ++v) {
-                rb[v] = *reinterpret_cast<const u32x4*>((const char*)(Bv + (size_t)(t0 + BR * v) * a.b_stride) + boff);
-                rc[v] = *reinterpret_cast<const u32x4*>((const char*)(Cv + (size_t)(t0 + BR * v) * a.c_stride) + coff);
-            }
-#pragma unroll
-            for (int v = 0; v < XV; ++v)
-                rx[v] = *reinterpret_cast<const u32x4*>((const char*)(X + (size_t)(t0 + XR * v) * a.x_stride) + xoff);
-        } else {
-#pragma unroll
-            for (int v = 0; v < BV; ++v) {
-                const uint32_t t = brow + BR * v, tt = t0 + (t < tl ? t : 0);
-                rb[v] = *reinterpret_cast<const u32x4*>(Bv + (size_t)tt * a.b_stride + bcol);
-                rc[v] = *reinterpret_cast<const u32x4*>(Cv + (size_t)tt * a.c_stride + bcol);
-            }
-#pragma unroll
-            for (int v = 0; v < XV; ++v) {
-                const uint32_t t = xrow + XR * v, tt = t0 + (t < tl ? t : 0);
-                rx[v] = *reinterpret_cast<const u32x4*>(X + (size_t)tt * a.x_stride + xcol);
-            }
+        for (int v = 0; v < BV; ++v) {
+            rb[v] = __builtin_amdgcn_raw_buffer_load_b128(rB, boff, v * bstep, 0);
+            rc[v] = __builtin_amdgcn_raw_buffer_load_b128(rC, coff, v * cstep, 0);
         }
-        if (w == 0) rdt = raw_of(dtr + (size_t)(t0 + min((uint32_t)lane, tl - 1)) * a.dt_stride);
+#pragma unroll
+        for (int v = 0; v < XV; ++v) rx[v] = __builtin_amdgcn_raw_buffer_load_b128(rX, xoff, v * xstep, 0);
+        const auto rD = rsrc(dtr + (size_t)t0 * a.dt_stride, ((tl - 1) * a.dt_stride + 1) * sizeof(T));
+        rdt = __builtin_amdgcn_raw_buffer_load_b16(rD, (uint32_t)lane * a.dt_stride * (uint32_t)sizeof(T), 0, 0);
     };
     auto stage = [&]() {
         if constexpr (GP) {
@@ -506,33 +528,69 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
 #pragma unroll
         for (int v = 0; v < XV; ++v) *reinterpret_cast<u32x4*>(Xs + (xrow + XR * v) * XP + xcol) = rx[v];
     };
-    // Wave 0: DT, Lcum, e^{Lcum} and the state weights w of the chunk at t0
-    // into buffer `buf` (tokens past tl get DT = 0, so they drop out).
-    auto scan = [&](uint32_t t0, int buf) {
+    // DT, Lcum, e^{Lcum}, the state weights w and the masked-decay factors of
+    // the chunk at t0 into buffer `buf` (tokens past tl get DT = 0, so they
+    // drop out).  Every wave forms DT and Lcum (a few instructions and a DPP
+    // prefix sum) and writes one part of the outputs, so the exponentials are
+    // spread over the waves: part 0 Lcum, DT and the block flags; 1 e^{Lcum}
+    // and w; 2 the row factors and the first column factors; 3 the others.
+    auto scan = [&](uint32_t t0, int buf, int part) {
         const uint32_t tl = min((uint32_t)CQ, L - t0);
         float dv = 0.0f;
         if ((uint32_t)lane < tl) {
-            dv = softplus_f(f_of<T>(rdt) + dt_b);
+            dv = softplus_fast(f_of<T>(rdt) + dt_b);
             dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
         }
-        float v = A_h * dv;
+        const float v = wave_prefix_sum(A_h * dv);
+        // factors of the masked decay.  Off-diagonal tiles (j < r <= t): both
+        // exponents <= 0, so a <= 1 and b <= DT.  Diagonal tiles (r <= j, t <
+        // r + 16): b >= DT grows with the block's decay, bounded by e^60 DT
+        // where the flag is set; tokens past tl have a = b = 0 (DT = 0).
+        if (part == 0) {
+            LCb[buf][lane] = v;
+            DTb[buf][lane] = dv;
+            const float lc_q = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x15F, 0xF, 0xF, false));
+            const float lc_r = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150, 0xF, 0xF, false));
+            const uint64_t ok = __ballot(lc_r - lc_q <= 60.0f);   // decay over the lane's block
+            if (lane == 0) {
+                uint32_t bits = 0;
 #pragma unroll
-        for (int off = 1; off < WAVE; off <<= 1) {
-            const float o = __shfl_up(v, off, WAVE);
-            if (lane >= off) v += o;
+                for (int tb = 0; tb < 4; ++tb) bits |= ((ok >> (16 * tb)) & 1ull) ? (1u << tb) : 0u;
+                SFb[buf] = bits;
+            }
+        } else if (part == 1) {
+            ELb[buf][lane] = __expf(v);
+            Wb[buf][lane] = __expf(readlane_f(v, WAVE - 1) - v) * dv;
+        } else if (part == 2) {
+            const float lc_r = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150, 0xF, 0xF, false));
+            AFb[buf][lane] = (uint32_t)lane < tl ? __expf(v - lc_r) : 0.0f;
+            BFb[buf][0][lane] = lane < 16 ? __expf(readlane_f(v, 0) - v) * dv : 0.0f;
+        } else {
+#pragma unroll
+            for (int tb = 1; tb < 4; ++tb)
+                BFb[buf][tb][lane] = lane < 16 * tb + 16 ? __expf(readlane_f(v, 16 * tb) - v) * dv : 0.0f;
         }
-        const float l_end = __shfl(v, WAVE - 1, WAVE);
-        LCb[buf][lane] = v;
-        DTb[buf][lane] = dv;
-        ELb[buf][lane] = __expf(v);
-        Wb[buf][lane] = __expf(l_end - v) * dv;
+    };
+    // the parts of the scan this wave writes
+    auto scan_parts = [&](uint32_t t0, int buf) {
+        if constexpr (NWV >= 4) {
+            if (w < 4) scan(t0, buf, w);
+        } else {
+            scan(t0, buf, w);
+            scan(t0, buf, w + 2);
+        }
     };
 
+    // Prefetches past the segment's last chunk re-read that chunk: loads
+    // issued on every iteration keep the registers they fill out of
+    // conditional merges (which the compiler resolves with copies that wait
+    // for the loads just issued).
+    const uint32_t t_last = (ce - 1) * CQ;
     fetch(cb * CQ);
     stage();
-    if (w == 0) scan(cb * CQ, 0);
-    if (cb + 1 < ce) fetch((cb + 1) * CQ);
-    __syncthreads();
+    scan_parts(cb * CQ, 0);
+    fetch(min((cb + 1) * CQ, t_last));
+    lds_barrier();
 
     for (uint32_t c = cb; c < ce; ++c) {
         const uint32_t par = (c - cb) & 1;   // buffer of this chunk's scalars
@@ -551,6 +609,7 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
         // would also wait for the prefetch). ----
         {
             const float* DTs = DTb[par];
+            const uint32_t safe = SFb[par];
 #pragma unroll
             for (int i = 0; i < NTL; ++i) {
                 const int kt = w + NWV * i;
@@ -571,25 +630,35 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
                             acc = mma16<T>(af, bf, acc);
                         }
                     }
-                    const float lct = LCs[t];
-                    const floatx4 lcj = *reinterpret_cast<const floatx4*>(LCs + 16 * J + 4 * lq);
-                    const floatx4 dtj = *reinterpret_cast<const floatx4*>(DTs + 16 * J + 4 * lq);
                     floatx4 m;
+                    if (J < Tt || ((safe >> Tt) & 1u)) {
+                        // factored decay (wave-uniform branch): two products
+                        const float at = AFb[par][t];
+                        const floatx4 bj = *reinterpret_cast<const floatx4*>(&BFb[par][Tt][16 * J + 4 * lq]);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int j = 16 * J + 4 * lq + r;
-                        // Lcum is non-increasing, so the exponent is <= 0 on
-                        // the kept entries; the clamp keeps the others finite
-                        float mv = acc[r] * __expf(fminf(lct - lcj[r], 0.0f)) * dtj[r];
-                        asm volatile("" : "+v"(mv));   // compute, then select (no branch)
-                        m[r] = (j <= t && (uint32_t)t < tl) ? mv : 0.0f;
+                        for (int r = 0; r < 4; ++r) {
+                            const float mv = acc[r] * at * bj[r];
+                            m[r] = (J < Tt || 16 * J + 4 * lq + r <= t) ? mv : 0.0f;
+                        }
+                    } else {
+                        const float lct = LCs[t];
+                        const floatx4 lcj = *reinterpret_cast<const floatx4*>(LCs + 16 * J + 4 * lq);
+                        const floatx4 dtj = *reinterpret_cast<const floatx4*>(DTs + 16 * J + 4 * lq);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int j = 16 * J + 4 * lq + r;
+                            // Lcum is non-increasing, so the exponent is <= 0 on
+                            // the kept entries; the clamp keeps the others finite
+                            float mv = acc[r] * __expf(fminf(lct - lcj[r], 0.0f)) * dtj[r];
+                            asm volatile("" : "+v"(mv));   // compute, then select (no branch)
+                            m[r] = (j <= t && (uint32_t)t < tl) ? mv : 0.0f;
+                        }
                     }
                     m4 = pack4<T>(m);
                 }
                 *reinterpret_cast<s4v*>(Ms + t * MPAD + 16 * J + 4 * lq) = m4;
             }
         }
-        if (w == 0 && c + 1 < ce) scan(t0 + CQ, par ^ 1);
 
         // ---- X^T slices of this wave's columns (k = token) ----
         s8v xf[2];
@@ -628,11 +697,13 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
             for (int ka = 0; ka < 2; ++ka) {
                 const floatx4 w0 = *reinterpret_cast<const floatx4*>(Ws + 32 * ka + 8 * lq);
                 const floatx4 w1 = *reinterpret_cast<const floatx4*>(Ws + 32 * ka + 8 * lq + 4);
+                floatx4 p0, p1;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    wx[ka][e] = bits_of<T>(w0[e] * val_of<T>(xf[ka][e]));
-                    wx[ka][e + 4] = bits_of<T>(w1[e] * val_of<T>(xf[ka][e + 4]));
+                    p0[e] = w0[e] * val_of<T>(xf[ka][e]);
+                    p1[e] = w1[e] * val_of<T>(xf[ka][e + 4]);
                 }
+                wx[ka] = cat8(pack4<T>(p0), pack4<T>(p1));
             }
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
@@ -650,7 +721,7 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
                 if constexpr (SPL == 2) Sx[(w * NST + nt % NST) * 64 + lane] = sp[nt];
             }
         }
-        __syncthreads();   // M complete; staging no longer read; state halves posted
+        lds_barrier();   // M complete; staging no longer read; state halves posted
         if constexpr (SPL == 2) {
             const int pw2 = (w + NW) % NWV;                 // the partner wave
 #pragma unroll
@@ -662,6 +733,9 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
         // waiting for them before the Y stores below keeps those stores out
         // of the wait.
         if (c + 1 < ce) stage();
+        // the next chunk's scalars (their buffer was last read in the previous
+        // chunk; dt arrived with the prefetch a chunk ago)
+        if (c + 1 < ce) scan_parts(t0 + CQ, par ^ 1);
 
         // ---- Y^T += X^T M^T + X^T (D I), store ----
 #pragma unroll
@@ -678,8 +752,8 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
             if ((uint32_t)t < tl)
                 *reinterpret_cast<s4v*>(Y + (size_t)(t0 + t) * a.y_stride + pw + 4 * lq) = pack4<T>(yacc[Tt]);
         }
-        if (c + 2 < ce) fetch(t0 + 2 * CQ);
-        __syncthreads();
+        fetch(min(t0 + 2 * CQ, t_last));
+        lds_barrier();
     }
     if (!last_seg) return;
 #pragma unroll
@@ -776,16 +850,11 @@ __global__ __launch_bounds__(64 * NW) void ssd_seg_state_kernel(SsdArgs a) {
         const uint32_t tl = min((uint32_t)CQ, L - t0);
         float dv = 0.0f;
         if ((uint32_t)lane < tl) {
-            dv = softplus_f(f_of<T>(rdt) + dt_b);
+            dv = softplus_fast(f_of<T>(rdt) + dt_b);
             dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
         }
-        float v = A_h * dv;
-#pragma unroll
-        for (int off = 1; off < WAVE; off <<= 1) {
-            const float o = __shfl_up(v, off, WAVE);
-            if (lane >= off) v += o;
-        }
-        const float l_end = __shfl(v, WAVE - 1, WAVE);
+        const float v = wave_prefix_sum(A_h * dv);
+        const float l_end = readlane_f(v, WAVE - 1);
         Wb[buf][lane] = __expf(l_end - v) * dv;
         if (lane == 0) LEb[buf] = l_end;
     };
@@ -951,16 +1020,11 @@ __global__ __launch_bounds__(256) void ssd_chunk_f32_mfma_kernel(SsdArgs a) {
         if (w == 0) {
             float dv = 0.0f;
             if ((uint32_t)lane < tl) {
-                dv = softplus_f(dtr[(size_t)(t0 + lane) * a.dt_stride] + dt_b);
+                dv = softplus_fast(dtr[(size_t)(t0 + lane) * a.dt_stride] + dt_b);
                 dv = fminf(fmaxf(dv, a.dt_min), a.dt_max);
             }
-            float v = A_h * dv;
-#pragma unroll
-            for (int off = 1; off < WAVE; off <<= 1) {
-                const float o = __shfl_up(v, off, WAVE);
-                if (lane >= off) v += o;
-            }
-            const float l_end = __shfl(v, WAVE - 1, WAVE);
+            const float v = wave_prefix_sum(A_h * dv);
+            const float l_end = readlane_f(v, WAVE - 1);
             LCs[lane] = v;
             DTs[lane] = dv;
             ELs[lane] = expf(v);
