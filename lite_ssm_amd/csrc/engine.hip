@@ -74,6 +74,14 @@ struct lssm_engine {
     float* seg = nullptr;      // prefill: the chunked scan's segment workspace
     // prefill: the split-K slices of GEMMs whose grid leaves most CUs idle
     float* gemm_ws = nullptr;
+    // prefill: the gated RMSNorm fused into the chunked scan's Y stores (which
+    // then hold r(g w), g = r(silu(z) r(y))) with each row's sums of g^2 per
+    // scan block (gpart) and 1 / rms per row (g_rs), applied by out_proj to
+    // its fp32 sums; where the scan cannot fuse it, the separate gated
+    // RMSNorm runs.  LSSM_FUSED_GATED_NORM=0 at creation turns it off.
+    float* gpart = nullptr;
+    float* g_rs = nullptr;
+    bool fuse_gated_norm = true;
     // batch-1 decode: in_proj, the SSD step (and out_proj) in one launch
     // (tagged words of each layer's projection and gated SSD output; the tag
     // is a count of batch-1 steps the embedding advances, so consecutive uses
@@ -378,11 +386,32 @@ struct lssm_engine {
             e = trace_rows(li, hidden, R);
             if (e == hipSuccess)
                 e = launch_rmsnorm(st(), hidden, d_model, w.norm_w, normed, d_model, R, d_model, RMS_EPS, act);
+            // the scan of this layer; with the gated norm fused into it, in_proj
+            // stores r(silu(z)) for the gate
+            SsdArgs s{xbc_act, xbc, (char*)xbc_act + (size_t)d_inner * es, xbc,
+                      (char*)xbc_act + (size_t)(d_inner + GN) * es, xbc,
+                      (char*)projb + (size_t)(d_inner + xbc) * es, proj, w.dt_bias, w.A_log, w.D,
+                      ys, d_inner, ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act,
+                      nullptr, 0, gram, seg};
+            uint32_t gparts = 0;   // the gated norm runs inside the scan (out_proj scales rows)
+            if (fuse_gated_norm && !fused) {
+                SsdArgs sg = s;
+                sg.z = projb;                                  // z: columns 0 .. d_inner of the projection
+                sg.z_stride = proj;
+                sg.gnorm_w = w.mixer_norm_w;
+                gparts = ssd_chunked_gate_parts(sg);
+                if (gparts) {
+                    s = sg;
+                    s.gpart = gpart;
+                    s.z_silu = true;
+                }
+            }
             if (e == hipSuccess && !fused) {
                 GemmArgs g{normed, d_model, w.in_proj_w, w.in_proj_s, projb, proj, nullptr, R, proj,
                            d_model, wfmt, act, LSSM_EPI_NONE, 1};
                 g.ws = gemm_ws;
                 g.ws_floats = GEMM_WS_FLOATS;
+                g.silu_cols = gparts ? d_inner : 0u;
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
             }
             if (e != hipSuccess) break;
@@ -395,22 +424,20 @@ struct lssm_engine {
                 if (e == hipSuccess)
                     e = launch_conv1d_seed(st(), xbc_pre, proj, conv_layer(li), B, L, xbc, K, act);
                 if (e == hipSuccess) {
-                    SsdArgs s{xbc_act, xbc, (char*)xbc_act + (size_t)d_inner * es, xbc,
-                              (char*)xbc_act + (size_t)(d_inner + GN) * es, xbc,
-                              (char*)projb + (size_t)(d_inner + xbc) * es, proj, w.dt_bias, w.A_log, w.D,
-                              ys, d_inner, ssd_layer(li), B, L, H, P, N, G, ck, DT_MIN, DT_MAX, 1u, act,
-                              nullptr, 0, gram, seg};
                     e = launch_ssd_chunked(st(), s);
+                    if (e == hipSuccess && gparts)
+                        e = launch_rms_from_parts(st(), gpart, gparts, R, d_inner, RMS_EPS, g_rs);
                 }
-                if (e == hipSuccess)
+                if (e == hipSuccess && !gparts)
                     e = launch_gated_rmsnorm(st(), projb, proj, ys, d_inner, w.mixer_norm_w, gn, R, d_inner,
                                              RMS_EPS, act);
             }
             if (e == hipSuccess) {
-                GemmArgs g{gn, d_inner, w.out_proj_w, w.out_proj_s, hidden, d_model, hidden, R, d_model,
-                           d_inner, wfmt, act, LSSM_EPI_ADD, 1};
+                GemmArgs g{gparts ? ys : gn, d_inner, w.out_proj_w, w.out_proj_s, hidden, d_model, hidden, R,
+                           d_model, d_inner, wfmt, act, LSSM_EPI_ADD, 1};
                 g.ws = gemm_ws;
                 g.ws_floats = GEMM_WS_FLOATS;
+                g.row_scale = gparts ? g_rs : nullptr;
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
             }
         }
@@ -578,6 +605,8 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A((void**)&e->gram, ssd_gram_floats(max_batch, max_seq, G) * sizeof(float));
     A((void**)&e->seg, ssd_seg_floats() * sizeof(float));
     A((void**)&e->gemm_ws, GEMM_WS_FLOATS * sizeof(float));
+    A((void**)&e->gpart, R * std::max<size_t>((size_t)e->H * e->P / 32, 1) * sizeof(float));
+    A((void**)&e->g_rs, R * sizeof(float));
     if (e->short_fused()) {
         const size_t R16 = (size_t)max_batch * 16;
         A(&e->f_z, R16 * d_inner * es);
@@ -615,6 +644,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     if (const char* v = getenv("LSSM_PARTS_MIN_ROWS")) e->parts_min_rows = (uint32_t)strtoul(v, nullptr, 10);
     if (const char* v = getenv("LSSM_GRAPH_UNROLL")) e->graph_unroll = (uint32_t)strtoul(v, nullptr, 10);
     if (const char* v = getenv("LSSM_NOPACK")) e->nopack = (int)strtol(v, nullptr, 10);
+    if (const char* v = getenv("LSSM_FUSED_GATED_NORM")) e->fuse_gated_norm = v[0] != '0';
     if (rc != LSSM_OK) {
         delete e;
         return rc;

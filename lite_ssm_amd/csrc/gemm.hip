@@ -206,6 +206,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs a) {
                 if (m < a.M && n < a.N) {
                     const size_t yi = (size_t)m * a.y_stride + n;
                     float v = acc[i][j][r];
+                    if (a.row_scale) v *= a.row_scale[m];
+                    if (n < a.silu_cols) v = silu_fast(v);
                     if (EPI == LSSM_EPI_SILU) v = silu_f(v);
                     if (EPI == LSSM_EPI_ADD) v = to_f(R[yi]) + rnd<T>(v);
                     Y[yi] = from_f<T>(v);
@@ -571,6 +573,13 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
         barrier();                                             // every wave's DMAs and reads done
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            // the row scales of this thread's 16 rows of the 32-row block i
+            float rsv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t rr = i * 32 + (r / 4) * 8 + (lane / 32) * 4 + r % 4;
+                rsv[r] = a.row_scale ? a.row_scale[min(m0 + wm * 128 + rr, a.M - 1)] : 1.0f;
+            }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const uint32_t c = wn * 64 + j * 32 + lane % 32;
@@ -578,6 +587,8 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t rr = i * 32 + (r / 4) * 8 + (lane / 32) * 4 + r % 4;
                     float v = acc[i][j][r];
+                    if (a.row_scale) v *= rsv[r];
+                    if (n0 + c < a.silu_cols) v = silu_fast(v);
                     if (EPI == LSSM_EPI_SILU) v = silu_f(v);
                     *reinterpret_cast<T*>(half + rr * RB + 16 * slot_of(rr, c / 8) + 2 * (c % 8)) = from_f<T>(v);
                 }
@@ -634,6 +645,8 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
                 if (m < a.M && n < a.N) {
                     const size_t yi = (size_t)m * a.y_stride + n;
                     float v = acc[i][j][r];
+                    if (a.row_scale) v *= a.row_scale[m];
+                    if (n < a.silu_cols) v = silu_fast(v);
                     if (EPI == LSSM_EPI_SILU) v = silu_f(v);
                     if (EPI == LSSM_EPI_ADD) v = to_f(Rz[yi]) + rnd<T>(v);
                     Y[yi] = from_f<T>(v);
@@ -763,6 +776,8 @@ __global__ __launch_bounds__(64 * SK_MAXW) void gemm_skinny_kernel(GemmArgs a) {
             if (nn >= a.N) continue;
             const size_t yi = (size_t)m * a.y_stride + nn;
             float o = v[rr];
+            if (a.row_scale) o *= a.row_scale[m];
+            if (nn < a.silu_cols) o = silu_fast(o);
             if (EPI == LSSM_EPI_SILU) o = silu_f(o);
             if (EPI == LSSM_EPI_ADD) o = to_f(R[yi]) + rnd<T>(o);
             Y[yi] = from_f<T>(o);
@@ -804,6 +819,8 @@ __global__ void gemm_simple_kernel(GemmArgs a) {
     }
     const size_t yi = (size_t)m * a.y_stride + n;
     float v = acc;
+    if (a.row_scale) v *= a.row_scale[m];
+    if (n < a.silu_cols) v = silu_fast(v);
     if (EPI == LSSM_EPI_SILU) v = silu_f(v);
     if (EPI == LSSM_EPI_ADD) v = to_f(((const T*)a.res)[yi]) + rnd<T>(v);
     ((T*)a.y)[yi] = from_f<T>(v);
@@ -850,6 +867,8 @@ __global__ __launch_bounds__(256) void gemm_split_sum_kernel(GemmArgs a, uint32_
     for (uint32_t z = 0; z < S; ++z) v += a.ws[z * MN + i];
     const uint32_t m = (uint32_t)(i / a.N), n = (uint32_t)(i % a.N);
     const size_t yi = (size_t)m * a.y_stride + n;
+    if (a.row_scale) v *= a.row_scale[m];
+    if (n < a.silu_cols) v = silu_fast(v);
     if (EPI == LSSM_EPI_SILU) v = silu_f(v);
     if (EPI == LSSM_EPI_ADD) v = to_f(((const T*)a.res)[yi]) + rnd<T>(v);
     ((T*)a.y)[yi] = from_f<T>(v);
@@ -875,6 +894,8 @@ __global__ __launch_bounds__(256) void gemm_split_sum4_kernel(GemmArgs a, uint32
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         float x = v[e];
+        if (a.row_scale) x *= a.row_scale[m];
+        if (n + e < a.silu_cols) x = silu_fast(x);
         if (EPI == LSSM_EPI_SILU) x = silu_f(x);
         if (EPI == LSSM_EPI_ADD) x = to_f(((const T*)a.res)[yi + e]) + rnd<T>(x);
         o[e] = from_f<T>(x);
@@ -992,6 +1013,7 @@ hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
             a2.s = (const uint16_t*)a.s + (size_t)n1 * (a.K / gs);
             a2.y = (T*)a.y + n1;
             if (a.res) a2.res = (const T*)a.res + n1;
+            a2.silu_cols = a.silu_cols > n1 ? a.silu_cols - n1 : 0u;   // columns count from n1
             run_wide(a1);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;

@@ -176,6 +176,13 @@ struct GemmArgs {
     // few tiles then splits K into slices whose sums a second launch adds
     float* ws = nullptr;
     size_t ws_floats = 0;
+    // prefill GEMM, optional: each output row's sums are scaled by
+    // row_scale[row] before the epilogue (the RMSNorm's 1 / rms of an input
+    // stored as r(x w)); null: no scale
+    const float* row_scale = nullptr;
+    // prefill GEMM, optional: outputs of columns n < silu_cols are r(silu(v))
+    // (SiLU with the hardware exp and reciprocal) instead of r(v); 0: none
+    uint32_t silu_cols = 0;
 };
 hipError_t launch_gemm(hipStream_t s, const GemmArgs& a);
 // Workspace the engine gives launch_gemm for its split-K slices (floats).
@@ -222,12 +229,29 @@ struct SsdArgs {
     void* yfrag = nullptr;
     float* ypart = nullptr;
     const void* ynorm_w = nullptr;
+    // chunked scan, optional (where ssd_chunked_gate_parts says it applies):
+    // the gated RMSNorm's gate and weight fused into the Y stores,
+    //   Y = r(g gnorm_w),  g = r(silu(z) r(y)),  z = a.z (row stride z_stride),
+    // and every token's sum of g^2 over each block's columns into
+    // gpart[row][ssd_chunked_gate_parts(a)] (block index h * (P / PB) + pb);
+    // the 1 / rms scale is then applied by the GEMM that reads Y
+    const void* gnorm_w = nullptr;
+    float* gpart = nullptr;
+    // with gpart: z already holds r(silu(z)) (the projection's GEMM applied
+    // it), so g = r(z r(y))
+    bool z_silu = false;
 };
 hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a);
 // Partials per row a decode step with SsdArgs::yfrag writes (H P / 32), or 0
 // when it cannot.
 uint32_t ssd_step_parts(uint32_t H, uint32_t P, uint32_t N, int act);
 hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a);
+// Partial sums of squares per row that launch_ssd_chunked writes when a.gpart
+// is set, or 0 where it cannot fuse the gate (not the MFMA walk).
+uint32_t ssd_chunked_gate_parts(const SsdArgs& a);
+// rs[row] = 1 / sqrt(sum of part[row][0 .. nparts) / dim + eps)
+hipError_t launch_rms_from_parts(hipStream_t s, const float* part, uint32_t nparts, uint32_t rows,
+                                 uint32_t dim, float eps, float* rs);
 inline size_t ssd_gram_floats(uint32_t batch, uint32_t L, uint32_t G) {
     return (size_t)batch * ((L + 63) / 64) * G * 64 * 64;
 }

@@ -413,6 +413,9 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
     // block T's own decay is small enough for its diagonal tile to use them
     __shared__ __attribute__((aligned(16))) float AFb[2][CQ], BFb[2][4][CQ];
     __shared__ uint32_t SFb[2];
+    // gated epilogue (a.gpart): each column slice's per-token sums of g^2,
+    // double-buffered by chunk parity
+    __shared__ __attribute__((aligned(16))) float GQ[2][NW][CQ];
     // SPL = 2: each wave's updated state tiles for its partner
     __shared__ __attribute__((aligned(16))) s4v Sx[SPL == 2 ? NWV * NST * 64 : 1];
 
@@ -427,6 +430,9 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
     const T* Cv = (const T*)a.C + (size_t)b * L * a.c_stride + (size_t)g * CN;
     const T* dtr = (const T*)a.dt + (size_t)b * L * a.dt_stride + h;
     T* Y = (T*)a.Y + (size_t)b * L * a.y_stride + (size_t)h * P + p0;
+    const bool gate = a.gpart != nullptr;
+    const T* Z = gate ? (const T*)a.z + (size_t)b * L * a.z_stride + (size_t)h * P + p0 : nullptr;
+    const uint32_t npart = H * npb;
     float* st = a.state + (((size_t)b * H + h) * P + p0) * CN;
     // segment blockIdx.z of a.nseg: chunks cb .. ce - 1, starting from the
     // state the segment pass left in the workspace; only the last segment
@@ -586,6 +592,30 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
     // conditional merges (which the compiler resolves with copies that wait
     // for the loads just issued).
     const uint32_t t_last = (ce - 1) * CQ;
+    // gated epilogue: the norm weights of this lane's four columns, and z of
+    // the wave's token tiles, requested at the start of each chunk (a phase
+    // ahead of their use in the Y stores)
+    floatx4 gw = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (gate) gw = unpack4<T>(*reinterpret_cast<const s4v*>((const T*)a.gnorm_w + (size_t)h * P + p0 + pw + 4 * lq));
+    typedef uint32_t u32x2z __attribute__((ext_vector_type(2)));
+    u32x2z zr[4];
+    auto fetch_z = [&](uint32_t t0) {
+        const uint32_t tl = min((uint32_t)CQ, L - t0);
+        const auto rZ = rsrc(Z + (size_t)t0 * a.z_stride, ((tl - 1) * a.z_stride + PB) * sizeof(T));
+        const uint32_t zo = (li * a.z_stride + pw + 4 * lq) * sizeof(T);
+#pragma unroll
+        for (int Tt = 0; Tt < 4; ++Tt)
+            if (Tt / NTT == hh)
+                zr[Tt] = __builtin_amdgcn_raw_buffer_load_b64(rZ, zo, Tt * 16 * a.z_stride * sizeof(T), 0);
+    };
+    // wave 0: the block's per-token sums of chunk cp (parity pp) to gpart
+    auto flush_gq = [&](uint32_t cp, uint32_t pp) {
+        const uint32_t tp0 = cp * CQ, tlp = min((uint32_t)CQ, L - tp0);
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) v += GQ[pp][k][lane];
+        if ((uint32_t)lane < tlp) a.gpart[((size_t)b * L + tp0 + lane) * npart + (size_t)h * npb + pb] = v;
+    };
     fetch(cb * CQ);
     stage();
     scan_parts(cb * CQ, 0);
@@ -600,6 +630,10 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
         const float* LCs = LCb[par];
         const float* ELs = ELb[par];
         const float* Ws = Wb[par];
+        if (gate) {
+            fetch_z(t0);
+            if (w == 0 && c > cb) flush_gq(c - 1, par ^ 1);
+        }
 
         // ---- G^T tiles (J <= T) -> M.  Twelve tiles, wave w takes positions
         // w, w + NW, ...; positions 0 and 4 are the zero upper halves (1,0)
@@ -749,12 +783,31 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
                 yacc[Tt] = mma16<T>(xf[ka], mf, yacc[Tt]);
             }
             if (a.has_D) yacc[Tt] = mma16<T>(xf[Tt / 2], dfr[Tt % 2], yacc[Tt]);
-            if ((uint32_t)t < tl)
+            if (gate) {
+                // the gated RMSNorm's front half (gated_rmsnorm: g =
+                // r(silu(z) r(y)), then g w): r(g w) stored, sum of g^2 kept
+                // (z_silu: the projection GEMM stored r(silu(z)) already)
+                const floatx4 zf = unpack4<T>(__builtin_bit_cast(s4v, zr[Tt]));
+                floatx4 o;
+                float sq = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float g = rnd<T>((a.z_silu ? zf[r] : silu_fast(zf[r])) * rnd<T>(yacc[Tt][r]));
+                    o[r] = g * gw[r];
+                    sq = fmaf(g, g, sq);
+                }
+                sq = swap_add32(swap_add16(sq));   // the token's 16 columns
+                if (lq == 0) GQ[par][cs][t] = sq;
+                if ((uint32_t)t < tl)
+                    *reinterpret_cast<s4v*>(Y + (size_t)(t0 + t) * a.y_stride + pw + 4 * lq) = pack4<T>(o);
+            } else if ((uint32_t)t < tl) {
                 *reinterpret_cast<s4v*>(Y + (size_t)(t0 + t) * a.y_stride + pw + 4 * lq) = pack4<T>(yacc[Tt]);
+            }
         }
         fetch(min(t0 + 2 * CQ, t_last));
         lds_barrier();
     }
+    if (gate && w == 0) flush_gq(ce - 1, (ce - 1 - cb) & 1);
     if (!last_seg) return;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
@@ -1176,33 +1229,70 @@ static uint32_t pick_segments(const SsdArgs& a, size_t nblk0) {
     return (nch + K - 1) / K;                              // no empty segment
 }
 
+namespace {
+// A single partial chunk (L < 64, chunk == L) has the same rounding points as
+// chunk 64, so it also takes the MFMA path.
+bool chunk_ok(const SsdArgs& a) { return a.chunk == CQ || (a.chunk == a.L && a.L < CQ); }
+bool mfma_ok(const SsdArgs& a) {
+    return (a.act != LSSM_F32) && chunk_ok(a) && a.N == CN && (a.P % 32) == 0 && (a.x_stride % 8 == 0) &&
+           (a.b_stride % 8 == 0) && (a.c_stride % 8 == 0) && (a.y_stride % 4 == 0) &&
+           ((uintptr_t)a.X % 16 == 0) && ((uintptr_t)a.B % 16 == 0) && ((uintptr_t)a.C % 16 == 0) &&
+           ((uintptr_t)a.Y % 8 == 0) && ((uintptr_t)a.state % 16 == 0);
+}
+// Four waves (64 columns of P) per block when that still gives a block per
+// CU, or when segments make up the count; otherwise two, for more blocks.
+bool walk_nw4(const SsdArgs& a, size_t cus) {
+    const uint32_t nch = (a.L + CQ - 1) / CQ;
+    const size_t nb64 = (size_t)a.batch * a.H * (a.P / 64);
+    return (a.P % 64) == 0 && (nb64 >= cus || (a.seg && nch >= 2));
+}
+
+// rs[row] = 1 / sqrt(sum_k part[row][k] / dim + eps): one wave per row, lane
+// l adding parts l, l + 64, ..., then a fixed-order wave sum
+__global__ __launch_bounds__(256) void rms_from_parts_kernel(const float* __restrict__ part, uint32_t nparts,
+                                                             uint32_t rows, float inv_dim, float eps,
+                                                             float* __restrict__ rs) {
+    const uint32_t row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (row >= rows) return;
+    const float* p = part + (size_t)row * nparts;
+    float v = 0.0f;
+    for (uint32_t k = lane; k < nparts; k += WAVE) v += p[k];
+    v = wave_sum(v);
+    if (lane == 0) rs[row] = 1.0f / sqrtf(v * inv_dim + eps);
+}
+}  // namespace
+
+uint32_t ssd_chunked_gate_parts(const SsdArgs& a) {
+    if (a.batch == 0 || a.H == 0 || a.L == 0 || !mfma_ok(a)) return 0;
+    if (!a.z || !a.gnorm_w || a.z_stride % 4 != 0 || (uintptr_t)a.z % 8 != 0 ||
+        (uintptr_t)a.gnorm_w % 8 != 0)
+        return 0;
+    return a.H * (a.P / (walk_nw4(a, num_cus()) ? 64u : 32u));
+}
+
+hipError_t launch_rms_from_parts(hipStream_t s, const float* part, uint32_t nparts, uint32_t rows,
+                                 uint32_t dim, float eps, float* rs) {
+    if (rows == 0) return hipSuccess;
+    rms_from_parts_kernel<<<(rows + 3) / 4, 256, 0, s>>>(part, nparts, rows, 1.0f / (float)dim, eps, rs);
+    return hipGetLastError();
+}
+
 hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a0) {
     if (a0.batch == 0 || a0.H == 0 || a0.L == 0) return hipSuccess;
     SsdArgs a = a0;
     const uint32_t nch = (a.L + CQ - 1) / CQ;
     a.nseg = 1;
     a.seg_chunks = nch;
-    // A single partial chunk (L < 64, chunk == L) has the same rounding points
-    // as chunk 64, so it also takes the MFMA path.
-    const bool chunk_ok = a.chunk == CQ || (a.chunk == a.L && a.L < CQ);
-    const bool mfma_ok = (a.act != LSSM_F32) && chunk_ok && a.N == CN && (a.P % 32) == 0 &&
-                         (a.x_stride % 8 == 0) && (a.b_stride % 8 == 0) && (a.c_stride % 8 == 0) &&
-                         (a.y_stride % 4 == 0) && ((uintptr_t)a.X % 16 == 0) &&
-                         ((uintptr_t)a.B % 16 == 0) && ((uintptr_t)a.C % 16 == 0) &&
-                         ((uintptr_t)a.Y % 8 == 0) && ((uintptr_t)a.state % 16 == 0);
     const size_t cus = num_cus();
+    if (a.gpart && ssd_chunked_gate_parts(a) == 0) return hipErrorInvalidValue;
     // segment pass + the scan of the segments' states (a.nseg > 1)
     auto seg_scan = [&]() {
         const size_t n4 = (size_t)a.batch * a.H * a.P * CN / 4;
         ssd_seg_scan_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(a);
     };
-    if (mfma_ok) {
-        // Four waves (64 columns of P) per block when that still gives a
-        // block per CU, or when segments make up the count; otherwise two,
-        // for more blocks.
-        const size_t nb64 = (size_t)a.batch * a.H * (a.P / 64);
+    if (mfma_ok(a)) {
         const bool p64 = (a.P % 64) == 0;
-        const bool nw4 = p64 && (nb64 >= cus || (a.seg && nch >= 2));
+        const bool nw4 = walk_nw4(a, cus);
         const uint32_t pbw = nw4 ? 64 : 32;
         a.nseg = pick_segments(a, (size_t)a.batch * a.H * (a.P / pbw));
         a.seg_chunks = (nch + a.nseg - 1) / a.nseg;
@@ -1247,7 +1337,7 @@ hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a0) {
         else go(bf16{});
         return hipGetLastError();
     }
-    if (a.act == LSSM_F32 && chunk_ok && a.N == CN && (a.P % 64) == 0 && ((uintptr_t)a.state % 16 == 0) &&
+    if (a.act == LSSM_F32 && chunk_ok(a) && a.N == CN && (a.P % 64) == 0 && ((uintptr_t)a.state % 16 == 0) &&
         ((uintptr_t)a.Y % 16 == 0) && (a.y_stride % 4 == 0)) {
         a.nseg = pick_segments(a, (size_t)a.batch * a.H * (a.P / 64));
         a.seg_chunks = (nch + a.nseg - 1) / a.nseg;
