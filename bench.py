@@ -43,8 +43,8 @@ MFMA_FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "inproj_ssd_decode_traffic.json")
 # the sources the dominant decode kernel is built from: a recorded traffic
 # figure is used only while they are unchanged
-KERNEL_SOURCES = ["lite_ssm_amd/csrc/gemv.hip", "lite_ssm_amd/csrc/gemv_core.cuh",
-                  "lite_ssm_amd/csrc/common.cuh"]
+KERNEL_SOURCES = ["lite_ssm_amd/csrc/gemv.hip", "lite_ssm_amd/csrc/gemv_core.hpp",
+                  "lite_ssm_amd/csrc/common.hpp"]
 
 
 def log(msg):

@@ -1,4 +1,4 @@
-// common.cuh — device types, conversions and wave-level helpers for gfx950.
+// common.hpp — device types, conversions and wave-level helpers for gfx950.
 //
 // Activations live in HBM as fp16 (the reference's only activation type,
 // shaders/common.metal:4-9), bf16 or fp32; all math is fp32.  Rounding to the

@@ -7,7 +7,7 @@
 #include <initializer_list>
 #include <utility>
 
-#include "common.cuh"
+#include "common.hpp"
 #include "internal.hpp"
 
 namespace lssm {

@@ -4,7 +4,7 @@
 // One block per 32 projection columns (as the reference); the L x 32 fp32
 // projection tile stays in LDS and the depthwise conv reads it UNROUNDED
 // (fused.metal:140-149), so this op's rounding differs from the unfused chain.
-#include "common.cuh"
+#include "common.hpp"
 #include "internal.hpp"
 
 namespace lssm {

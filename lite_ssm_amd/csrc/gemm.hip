@@ -12,7 +12,7 @@
 // padded to 72 elements so the 16-byte fragment reads of 8 consecutive rows
 // hit distinct banks); the global loads of step k+1 are issued before the
 // MFMAs of step k.
-#include "common.cuh"
+#include "common.hpp"
 #include "internal.hpp"
 
 namespace lssm {

@@ -31,7 +31,7 @@
 //    lanes of a row fall in distinct banks; 16 lanes per row.
 #include <type_traits>
 
-#include "gemv_core.cuh"
+#include "gemv_core.hpp"
 
 namespace lssm {
 

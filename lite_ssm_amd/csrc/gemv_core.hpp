@@ -1,10 +1,10 @@
-// gemv_core.cuh — pieces shared by the decode GEMV kernels (gemv.hip: one
+// gemv_core.hpp — pieces shared by the decode GEMV kernels (gemv.hip: one
 // to four x rows on VALU; gemv_mma.hip: decode batches on MFMA): the weight
 // formats, the int4 / int8 unpack into packed fp16 / bf16 pairs and the order
 // of those pairs, and the per-row epilogues.
 #pragma once
 
-#include "common.cuh"
+#include "common.hpp"
 #include "internal.hpp"
 
 namespace lssm {

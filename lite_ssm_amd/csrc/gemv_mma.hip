@@ -4,7 +4,7 @@
 #include <algorithm>
 #include <cstdlib>
 
-#include "gemv_core.cuh"
+#include "gemv_core.hpp"
 
 namespace lssm {
 

@@ -13,7 +13,7 @@
 #include <cfloat>
 #include <cstdlib>
 
-#include "common.cuh"
+#include "common.hpp"
 #include "internal.hpp"
 
 namespace lssm {
