@@ -82,6 +82,16 @@ struct lssm_engine {
     float* gpart = nullptr;
     float* g_rs = nullptr;
     bool fuse_gated_norm = true;
+    // prefill: the next layer's pre-mixer RMSNorm folded into out_proj's
+    // epilogue, which then also writes normed = r(h w) and each row's sums of
+    // h^2 per 128 columns (hpart); 1 / rms per row (h_rs) is applied by the
+    // next in_proj to its fp32 sums.  Where the GEMM cannot fold it (and for
+    // the first layer) the separate RMSNorm runs.  Off by default (measured no
+    // faster at 4 x 4096: the epilogue's extra stores and the row scale cost
+    // what the norm pass did); LSSM_FOLD_PRE_NORM=1 at creation turns it on.
+    float* hpart = nullptr;
+    float* h_rs = nullptr;
+    bool fold_pre_norm = false;
     // batch-1 decode: in_proj, the SSD step (and out_proj) in one launch
     // (tagged words of each layer's projection and gated SSD output; the tag
     // is a count of batch-1 steps the embedding advances, so consecutive uses
@@ -381,10 +391,11 @@ struct lssm_engine {
         // fused in_proj + conv + SiLU split (its conv reads the unrounded
         // projection, so it rounds differently from the chain below)
         const bool fused = short_fused() && L > 1 && L <= 16;
+        bool normed_ready = false;   // the previous out_proj wrote normed and h_rs
         for (uint32_t li = 0; li < cfg.n_layer && e == hipSuccess; ++li) {
             const lssm_layer_weights& w = layers[li];
             e = trace_rows(li, hidden, R);
-            if (e == hipSuccess)
+            if (e == hipSuccess && !normed_ready)
                 e = launch_rmsnorm(st(), hidden, d_model, w.norm_w, normed, d_model, R, d_model, RMS_EPS, act);
             // the scan of this layer; with the gated norm fused into it, in_proj
             // stores r(silu(z)) for the gate
@@ -412,6 +423,7 @@ struct lssm_engine {
                 g.ws = gemm_ws;
                 g.ws_floats = GEMM_WS_FLOATS;
                 g.silu_cols = gparts ? d_inner : 0u;
+                g.row_scale = normed_ready ? h_rs : nullptr;
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
             }
             if (e != hipSuccess) break;
@@ -438,7 +450,17 @@ struct lssm_engine {
                 g.ws = gemm_ws;
                 g.ws_floats = GEMM_WS_FLOATS;
                 g.row_scale = gparts ? g_rs : nullptr;
+                normed_ready = false;
+                if (fold_pre_norm && !fused && li + 1 < cfg.n_layer) {
+                    g.y2 = normed;
+                    g.y2_w = layers[li + 1].norm_w;
+                    g.y2_part = hpart;
+                    normed_ready = gemm_norm_fold_takes(g);
+                    if (!normed_ready) g.y2 = nullptr;
+                }
                 e = (act == LSSM_F32) ? launch_gemm_simple(st(), g) : launch_gemm(st(), g);
+                if (e == hipSuccess && normed_ready)
+                    e = launch_rms_from_parts(st(), hpart, d_model / 128, R, d_model, RMS_EPS, h_rs);
             }
         }
         if (e == hipSuccess) e = trace_rows(cfg.n_layer, hidden, R);
@@ -607,6 +629,8 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A((void**)&e->gemm_ws, GEMM_WS_FLOATS * sizeof(float));
     A((void**)&e->gpart, R * std::max<size_t>((size_t)e->H * e->P / 32, 1) * sizeof(float));
     A((void**)&e->g_rs, R * sizeof(float));
+    A((void**)&e->hpart, R * std::max<size_t>(e->d_model / 128, 1) * sizeof(float));
+    A((void**)&e->h_rs, R * sizeof(float));
     if (e->short_fused()) {
         const size_t R16 = (size_t)max_batch * 16;
         A(&e->f_z, R16 * d_inner * es);
@@ -645,6 +669,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     if (const char* v = getenv("LSSM_GRAPH_UNROLL")) e->graph_unroll = (uint32_t)strtoul(v, nullptr, 10);
     if (const char* v = getenv("LSSM_NOPACK")) e->nopack = (int)strtol(v, nullptr, 10);
     if (const char* v = getenv("LSSM_FUSED_GATED_NORM")) e->fuse_gated_norm = v[0] != '0';
+    if (const char* v = getenv("LSSM_FOLD_PRE_NORM")) e->fold_pre_norm = v[0] != '0';
     if (rc != LSSM_OK) {
         delete e;
         return rc;

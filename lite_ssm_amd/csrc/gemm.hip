@@ -473,6 +473,17 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
         for (int j = j0; j < j1; ++j) lds_dma16_asm(base + xo[j], dst + 8 * j * G2K * (uint32_t)sizeof(T));
     };
 
+    // row scales of the wave's 128 tile rows, requested now and spread over
+    // the lanes (lane l: rows l and 64 + l of the half): the epilogue takes
+    // each row's from its lane by readlane instead of waiting, per 32-row
+    // block, on 16 scattered loads
+    float rs_lo = 1.0f, rs_hi = 1.0f;
+    if (a.row_scale && gridDim.z == 1) {
+        const uint32_t mb = m0 + wm * 128;
+        rs_lo = a.row_scale[min(mb + lane, a.M - 1)];
+        rs_hi = a.row_scale[min(mb + 64 + lane, a.M - 1)];
+    }
+
     floatx16 acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -573,12 +584,16 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
         barrier();                                             // every wave's DMAs and reads done
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            // the row scales of this thread's 16 rows of the 32-row block i
+            // the row scales of this thread's 16 rows of the 32-row block i:
+            // row rr of the half is lane rr % 64 of rs_lo (rr < 64) or rs_hi;
+            // lanes 0..31 take row r0, lanes 32..63 row r0 + 4
             float rsv[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t rr = i * 32 + (r / 4) * 8 + (lane / 32) * 4 + r % 4;
-                rsv[r] = a.row_scale ? a.row_scale[min(m0 + wm * 128 + rr, a.M - 1)] : 1.0f;
+                const uint32_t r0 = i * 32 + (r / 4) * 8 + r % 4, r1 = r0 + 4;
+                const float s0 = readlane_f(r0 < 64 ? rs_lo : rs_hi, (int)(r0 % 64));
+                const float s1 = readlane_f(r1 < 64 ? rs_lo : rs_hi, (int)(r1 % 64));
+                rsv[r] = lane < 32 ? s0 : s1;
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -598,6 +613,13 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
         barrier();
         constexpr uint32_t SPR = BN / 8;                       // slots per row
         constexpr uint32_t NT = 64 * CW;
+        // a thread's slot (NT % SPR == 0): the next norm's weights of its 8
+        // columns, one load for all its rows
+        u32x4 y2w{0u, 0u, 0u, 0u};
+        if (EPI == LSSM_EPI_ADD && a.y2) {
+            const uint32_t nw = n0 + 8 * (threadIdx.x % SPR);
+            if (nw + 8 <= a.N) y2w = *reinterpret_cast<const u32x4*>((const T*)a.y2_w + nw);
+        }
 #pragma unroll 4
         for (uint32_t q = threadIdx.x; q < G2M * SPR; q += NT) {
             const uint32_t R = q / SPR, sl = q % SPR, rr = R % 128;
@@ -618,6 +640,28 @@ __global__ __launch_bounds__(64 * (CW + 4)) void gemm2_kernel(GemmArgs a) {
                                ((uint32_t)__builtin_bit_cast(uint16_t, from_f<T>(hi)) << 16);
                     }
                     *reinterpret_cast<u32x4*>(Y + yi) = o;
+                    if (a.y2) {
+                        // the next RMSNorm's input r(y w) and the sums of y^2
+                        // over the 128 columns of this thread's 16-lane row
+                        // (the rows of a DPP row share m; N % 128 == 0)
+                        const u32x4 wv = y2w;
+                        u32x4 o2;
+                        float sq = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float lo = f_of_bits<T>((uint16_t)o[e]);
+                            const float hi = f_of_bits<T>((uint16_t)(o[e] >> 16));
+                            sq = fmaf(lo, lo, sq);
+                            sq = fmaf(hi, hi, sq);
+                            const float wl = f_of_bits<T>((uint16_t)wv[e]);
+                            const float wh = f_of_bits<T>((uint16_t)(wv[e] >> 16));
+                            o2[e] = (uint32_t)__builtin_bit_cast(uint16_t, from_f<T>(lo * wl)) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, from_f<T>(hi * wh)) << 16);
+                        }
+                        *reinterpret_cast<u32x4*>((T*)a.y2 + yi) = o2;
+                        sq = group_sum<16>(sq);
+                        if (threadIdx.x % 16 == 0) a.y2_part[(size_t)(n / 128) * a.M + m] = sq;
+                    }
                 } else {
                     *reinterpret_cast<u32x4*>(Y + yi) = st;
                 }
@@ -1014,6 +1058,11 @@ hipError_t go_epi(hipStream_t s, const GemmArgs& a) {
             a2.y = (T*)a.y + n1;
             if (a.res) a2.res = (const T*)a.res + n1;
             a2.silu_cols = a.silu_cols > n1 ? a.silu_cols - n1 : 0u;   // columns count from n1
+            if (a.y2) {
+                a2.y2 = (T*)a.y2 + n1;
+                a2.y2_w = (const T*)a.y2_w + n1;
+                a2.y2_part = a.y2_part + (size_t)(n1 / 128) * a.M;
+            }
             run_wide(a1);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
@@ -1044,8 +1093,21 @@ hipError_t go_fmt(hipStream_t s, const GemmArgs& a) {
 
 }  // namespace
 
+bool gemm_norm_fold_takes(const GemmArgs& a) {
+    const size_t es = 2;
+    if (a.act != LSSM_F16 && a.act != LSSM_BF16) return false;
+    if (a.epi != LSSM_EPI_ADD || !a.res || !a.y2 || !a.y2_w || !a.y2_part) return false;
+    if (a.M <= 128 || (uint64_t)a.M * a.x_stride * es >= (1ull << 31)) return false;
+    if (a.N % 128 != 0 || a.y_stride % 8 != 0) return false;
+    for (const void* p : {(const void*)a.y, a.res, (const void*)a.y2, a.y2_w})
+        if ((uintptr_t)p % 16 != 0) return false;
+    if (a.wfmt != LSSM_W_DENSE && gemm_split(a, a.wfmt == LSSM_W_Q4_G64 ? 64u : 32u) > 1) return false;
+    return true;
+}
+
 hipError_t launch_gemm(hipStream_t s, const GemmArgs& a) {
     if (a.M == 0 || a.N == 0) return hipSuccess;
+    if (a.y2 && !gemm_norm_fold_takes(a)) return hipErrorInvalidValue;
     if (a.act == LSSM_F16) return go_fmt<f16>(s, a);
     if (a.act == LSSM_BF16) return go_fmt<bf16>(s, a);
     return hipErrorInvalidValue;

@@ -183,7 +183,20 @@ struct GemmArgs {
     // prefill GEMM, optional: outputs of columns n < silu_cols are r(silu(v))
     // (SiLU with the hardware exp and reciprocal) instead of r(v); 0: none
     uint32_t silu_cols = 0;
+    // prefill GEMM with the residual add, optional (where gemm_norm_fold_takes
+    // says so): the next RMSNorm's input folded into the epilogue.  Besides
+    // y = r(res + r(v)) it writes y2 = r(y norm_w) (row stride y_stride) and
+    // each row's sum of y^2 over every 128 columns to
+    // y2_part[n / 128][M]; the GEMM that reads y2 then scales its sums by the
+    // row's 1 / rms (row_scale, from launch_rms_from_parts)
+    void* y2 = nullptr;
+    const void* y2_w = nullptr;
+    float* y2_part = nullptr;
 };
+// Whether launch_gemm runs a (with y2 set) through the epilogue that writes y2
+// and y2_part: bf16 / f16, the residual add, M > 128 without a K split,
+// N % 128 == 0, 16-byte aligned rows.  launch_gemm refuses y2 elsewhere.
+bool gemm_norm_fold_takes(const GemmArgs& a);
 hipError_t launch_gemm(hipStream_t s, const GemmArgs& a);
 // Workspace the engine gives launch_gemm for its split-K slices (floats).
 // The 130M prefill of 2048 tokens (config 3) runs its out_proj in four slices
@@ -233,7 +246,7 @@ struct SsdArgs {
     // the gated RMSNorm's gate and weight fused into the Y stores,
     //   Y = r(g gnorm_w),  g = r(silu(z) r(y)),  z = a.z (row stride z_stride),
     // and every token's sum of g^2 over each block's columns into
-    // gpart[row][ssd_chunked_gate_parts(a)] (block index h * (P / PB) + pb);
+    // gpart[part][batch L] (part = h * (P / PB) + pb, ssd_chunked_gate_parts(a) of them);
     // the 1 / rms scale is then applied by the GEMM that reads Y
     const void* gnorm_w = nullptr;
     float* gpart = nullptr;
@@ -249,7 +262,8 @@ hipError_t launch_ssd_chunked(hipStream_t s, const SsdArgs& a);
 // Partial sums of squares per row that launch_ssd_chunked writes when a.gpart
 // is set, or 0 where it cannot fuse the gate (not the MFMA walk).
 uint32_t ssd_chunked_gate_parts(const SsdArgs& a);
-// rs[row] = 1 / sqrt(sum of part[row][0 .. nparts) / dim + eps)
+// rs[row] = 1 / sqrt(sum of part[0 .. nparts)[row] / dim + eps), part[k] a
+// column of `rows` floats
 hipError_t launch_rms_from_parts(hipStream_t s, const float* part, uint32_t nparts, uint32_t rows,
                                  uint32_t dim, float eps, float* rs);
 inline size_t ssd_gram_floats(uint32_t batch, uint32_t L, uint32_t G) {

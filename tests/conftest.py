@@ -33,6 +33,21 @@ def pytest_terminal_summary(terminalreporter):
                 f.write(json.dumps(r, sort_keys=True, default=float) + "\n")
 
 
+@pytest.fixture(scope="session")
+def progress(request):
+    """say(msg): print a progress line past pytest's output capture, so that a
+    test which runs for minutes shows on the console that it is advancing."""
+    capman = request.config.pluginmanager.getplugin("capturemanager")
+
+    def say(msg):
+        if capman is None:
+            print(msg, flush=True)
+            return
+        with capman.global_and_fixture_disabled():
+            print(msg, flush=True)
+    return say
+
+
 @pytest.fixture
 def parity_record():
     """record(name, **figures): keep a test's parity figures for the summary."""

@@ -312,6 +312,52 @@ def test_engine_normalise_on_load_decode(ctx, monkeypatch, name, B):
         assert same >= bound, f"layer {li - 1}: only {same:.4f} of the hidden elements match the raw-pack path"
 
 
+def test_engine_prefill_folded_norms(ctx, monkeypatch):
+    """Both RMSNorms of a prefill layer folded into their neighbours: out_proj's
+    epilogue writes the next layer's r(h w) with sums of h^2 per 128 columns
+    and the next in_proj scales its fp32 sums by 1 / rms; the chunked scan's Y
+    stores hold the gated norm's r(g w) with sums of g^2 and out_proj scales
+    by that 1 / rms.  Full-width 2.7B layers at 1600 rows (7 row tiles: the
+    out_proj GEMM runs unsplit, so the fold is taken): every layer against the
+    oracle's run_block on the engine's own input rows, and against an engine
+    with both folds off (LSSM_FOLD_PRE_NORM=0, LSSM_FUSED_GATED_NORM=0), which
+    must differ (the folds ran) but stay within the bound."""
+    from lite_ssm_amd.model import Engine
+    print("case: folded prefill norms, 2.7B widths, 3 layers, 1 x 1600", flush=True)
+    L, sh, m, om = _setup(ctx, "mamba2-2.7b", O.BF16, O.W_Q4_G64, n_layer=3, vocab_size=512, seed=37)
+    B, Lq = 1, 1600
+    ids = np.random.default_rng(9).integers(0, sh.vocab_size, (B, Lq)).astype(np.int32)
+    traces = {}
+    for mode in ("off", "on"):
+        v = "0" if mode == "off" else "1"
+        monkeypatch.setenv("LSSM_FOLD_PRE_NORM", v)
+        monkeypatch.setenv("LSSM_FUSED_GATED_NORM", v)
+        eng = Engine(ctx, m, max_batch=B, max_seq=Lq)
+        try:
+            tr = torch.zeros((sh.n_layer + 1, B * Lq, sh.d_model), dtype=torch.bfloat16, device="cuda")
+            eng.set_trace(tr)
+            nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+            eng.prefill(torch.from_numpy(ids).cuda(), nxt)
+            eng.set_trace(None)
+            traces[mode] = tr.view(torch.int16).cpu().numpy()
+        finally:
+            eng.close()
+    on, off = traces["on"], traces["off"]
+    assert np.array_equal(on[0], off[0]), "the embedding rows differ"
+    conv, ssd = om.new_state(B)
+    for li in range(sh.n_layer):
+        h = np.ascontiguousarray(on[li])
+        om.block(li, h, conv, ssd, B, Lq, False)
+        e = max_rel(O.from_act(h, O.BF16), O.from_act(on[li + 1], O.BF16))
+        d = max_rel(O.from_act(on[li + 1], O.BF16), O.from_act(off[li + 1], O.BF16))
+        same = float(np.mean(on[li + 1] == off[li + 1]))
+        print(f"layer {li}: folded against the oracle {e:.2e}, against unfolded {d:.2e} "
+              f"({same:.3f} of elements equal)", flush=True)
+        assert e <= MAXREL[O.BF16], f"layer {li}: output max-rel {e:.3e} against the oracle"
+        assert d <= MAXREL[O.BF16], f"layer {li}: folded and unfolded differ by {d:.3e}"
+    assert not np.array_equal(on[2], off[2]), "the second layer's rows are bit-identical: no fold ran"
+
+
 def test_engine_one_token_prefill(ctx):
     """L == 1 prefill takes the reference's GEMV / conv-update / SSD-step path
     and seeds the conv state (mamba2_block.cpp:111-116, 155-162, 183-195, 285-289)."""

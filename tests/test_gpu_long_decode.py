@@ -148,9 +148,10 @@ def _host_state(eng, B):
 
 
 @pytest.fixture(scope="module")
-def m2p7b_walk(torch_cuda):
+def m2p7b_walk(torch_cuda, progress):
+    say = progress
     from lite_ssm_amd.model import DeviceModel, shape
-    print("building 2.7B-shaped model (permuted head)", flush=True)
+    say("building 2.7B-shaped model (permuted head)")
     sh = shape("mamba2-2.7b")
     m = DeviceModel(sh, act=O.BF16, wfmt=O.W_Q4_G64, seed=21, embed_std=1.5, head="permuted")
     om = O.Model(m.to_host(), vars(sh), O.BF16, O.W_Q4_G64)
@@ -159,11 +160,12 @@ def m2p7b_walk(torch_cuda):
 
 
 @pytest.mark.timeout(1200)
-def test_decode_2p7b_bs1_512_free_running(ctx, m2p7b_walk, parity_record):
+def test_decode_2p7b_bs1_512_free_running(ctx, m2p7b_walk, parity_record, progress):
+    say = progress
     from lite_ssm_amd.model import Engine
     sh, m, om = m2p7b_walk
     Lp, steps, chunk = 16, 512, 128
-    print(f"case: 2.7B batch 1, prefill {Lp}, {steps} free-running steps (4-step graphs)", flush=True)
+    say(f"case: 2.7B batch 1, prefill {Lp}, {steps} free-running steps (4-step graphs)")
     prompt = torch.randint(0, sh.vocab_size, (1, Lp), generator=torch.Generator().manual_seed(77),
                            dtype=torch.int32)
     eng = Engine(ctx, m, 1, Lp)
@@ -182,7 +184,7 @@ def test_decode_2p7b_bs1_512_free_running(ctx, m2p7b_walk, parity_record):
         g_ids = [id0] + [int(v) for v in log[:, 0].cpu()]
         gconv, gssd = eng.state()
         eng.set_id_log(None)
-        print(f"graph run done: fused layers {fused}, ids[:8] {g_ids[:8]}", flush=True)
+        say(f"graph run done: fused layers {fused}, ids[:8] {g_ids[:8]}")
         assert fused == sh.n_layer, "the fused in_proj + SSD launch did not run"
         assert min(g_ids) >= 0
 
@@ -218,7 +220,7 @@ def test_decode_2p7b_bs1_512_free_running(ctx, m2p7b_walk, parity_record):
     for c, (trace, (c0, s0), (c1, s1)) in kept.items():
         layer_errs[c] = [round(v, 5) for v in
                          _layers_from_engine_state(om, trace, c0, s0, c1, s1, 1, f"step {c}")]
-        print(f"step {c}: worst layer output / SSD / conv max-rel {layer_errs[c]}", flush=True)
+        say(f"step {c}: worst layer output / SSD / conv max-rel {layer_errs[c]}")
     del kept
 
     # the whole model: the oracle's own 64 layers (twice), fed the engine's ids
@@ -245,9 +247,9 @@ def test_decode_2p7b_bs1_512_free_running(ctx, m2p7b_walk, parity_record):
             flips += 1
             if first is None:
                 first = (s, gap, err_abs)
-        if s % 128 == 0:
-            print(f"oracle at step {s}: logits max-rel so far {max(errs):.2e} (oracle f32 against f64 "
-                  f"{max(orc.yard):.2e}), flips {flips}", flush=True)
+        if s % 32 == 0:
+            say(f"oracle at step {s}: logits max-rel so far {max(errs):.2e} (oracle f32 against f64 "
+                  f"{max(orc.yard):.2e}), flips {flips}")
     conv, ssd = orc.st[0]
     e_ssd, e_conv = _state_errs(om, gconv, gssd, conv, ssd, 1)
     y_ssd, y_conv = orc.state_yard()
@@ -270,7 +272,7 @@ def test_decode_2p7b_bs1_512_free_running(ctx, m2p7b_walk, parity_record):
     assert len(set(g_ids)) >= 64, f"only {len(set(g_ids))} distinct ids in {steps + 1} steps"
 
 
-def _teacher_forced(ctx, sh, m, om, B, Lp, steps, seed, what, parity_record):
+def _teacher_forced(ctx, sh, m, om, B, Lp, steps, seed, what, parity_record, say):
     """Prefill Lp tokens per sequence, then `steps` eager decode steps with
     given ids: whole-model logits of every sequence at every step; every layer
     at the middle and last steps from the engine's own state; then graph
@@ -302,7 +304,7 @@ def _teacher_forced(ctx, sh, m, om, B, Lp, steps, seed, what, parity_record):
                 c1, s1 = _host_state(eng, B)
                 layer_errs[s] = [round(v, 5) for v in _layers_from_engine_state(
                     om, _bits(tr).copy(), c0, s0, c1, s1, B, f"{what} step {s}")]
-                print(f"{what} step {s}: worst layer output / SSD / conv max-rel {layer_errs[s]}", flush=True)
+                say(f"{what} step {s}: worst layer output / SSD / conv max-rel {layer_errs[s]}")
             g = eng.logits(B).float().cpu().numpy()
             ref = orc.decode(tf[s - 1].numpy())
             assert np.all(np.isfinite(g)), f"{what} step {s}: non-finite logits"
@@ -315,9 +317,9 @@ def _teacher_forced(ctx, sh, m, om, B, Lp, steps, seed, what, parity_record):
                     id_checked += 1
                     assert gid[r] == int(np.argmax(ref[r])), f"{what} step {s}: greedy id of row {r}"
                     id_same += 1
-            if s % 16 == 0:
-                print(f"{what}: step {s}, whole-model logits max-rel so far {max(errs):.2e} (oracle f32 "
-                      f"against f64 {max(orc.yard):.2e})", flush=True)
+            if s % 4 == 0:
+                say(f"{what}: step {s}, whole-model logits max-rel so far {max(errs):.2e} (oracle f32 "
+                      f"against f64 {max(orc.yard):.2e})")
         gconv, gssd = eng.state()
         conv, ssd = orc.st[0]
         e_ssd, e_conv = _state_errs(om, gconv, gssd, conv, ssd, B)
@@ -362,25 +364,29 @@ def _teacher_forced(ctx, sh, m, om, B, Lp, steps, seed, what, parity_record):
 
 
 @pytest.mark.timeout(1200)
-def test_decode_2p7b_bs16_128_teacher_forced(ctx, m2p7b_walk, parity_record):
+def test_decode_2p7b_bs16_128_teacher_forced(ctx, m2p7b_walk, parity_record, progress):
+    say = progress
     sh, m, om = m2p7b_walk
-    print("case: 2.7B batch 16, prefill 8, 128 teacher-forced steps", flush=True)
-    _teacher_forced(ctx, sh, m, om, 16, 8, 128, 81, "2.7B bs16", parity_record)
+    say("case: 2.7B batch 16, prefill 8, 128 teacher-forced steps")
+    _teacher_forced(ctx, sh, m, om, 16, 8, 128, 81, "2.7B bs16", parity_record, say)
 
 
 @pytest.fixture(scope="module")
-def m8b_long(torch_cuda):
+def m8b_long(torch_cuda, progress):
+    say = progress
     from lite_ssm_amd.model import DeviceModel, shape
-    print("building 8B-shaped model", flush=True)
+    say("building 8B-shaped model")
     sh = shape("mamba2-8b")
     m = DeviceModel(sh, act=O.BF16, wfmt=O.W_Q4_G64, seed=31)
     om = O.Model(m.to_host(), vars(sh), O.BF16, O.W_Q4_G64)
+    say("8B-shaped model built on the device and in the oracle")
     yield sh, m, om
     del m
 
 
 @pytest.mark.timeout(1200)
-def test_decode_8b_bs32_32_teacher_forced(ctx, m8b_long, parity_record):
+def test_decode_8b_bs32_32_teacher_forced(ctx, m8b_long, parity_record, progress):
+    say = progress
     sh, m, om = m8b_long
-    print("case: 8B batch 32, prefill 4, 32 teacher-forced steps", flush=True)
-    _teacher_forced(ctx, sh, m, om, 32, 4, 32, 91, "8B bs32", parity_record)
+    say("case: 8B batch 32, prefill 4, 32 teacher-forced steps")
+    _teacher_forced(ctx, sh, m, om, 32, 4, 32, 91, "8B bs32", parity_record, say)
