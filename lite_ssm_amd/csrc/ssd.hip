@@ -1251,23 +1251,34 @@ bool walk_nw4(const SsdArgs& a, size_t cus) {
     return (a.P % 64) == 0 && (nb64 >= cus || (a.seg && nch >= 2));
 }
 
-// rs[row] = 1 / sqrt(sum_k part[k][row] / dim + eps): one thread per row,
-// adding the parts in order k = 0, 1, ... in four interleaved sums (a wave's
-// loads of one part are 256 consecutive bytes)
+// rs[row] = 1 / sqrt(sum_k part[k][row] / dim + eps).  A block takes 64 rows;
+// wave w adds parts w, w + 4, ... of its lane's row (each load instruction
+// reads 256 consecutive bytes), then the four waves' sums meet in LDS in a
+// fixed order.
 __global__ __launch_bounds__(256) void rms_from_parts_kernel(const float* __restrict__ part, uint32_t nparts,
                                                              uint32_t rows, float inv_dim, float eps,
                                                              float* __restrict__ rs) {
-    const uint32_t row = blockIdx.x * 256 + threadIdx.x;
-    if (row >= rows) return;
-    const float* p = part + row;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t k = 0;
-    for (; k + 4 <= nparts; k += 4) {
+    __shared__ float red[4][64];
+    const uint32_t lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
+    const uint32_t row = blockIdx.x * 64 + lane;
+    float v = 0.0f;
+    if (row < rows) {
+        // eight loads in flight, added in the order of k
+        const float* p = part + row;
+        uint32_t k = w;
+        for (; k + 28 < nparts; k += 32) {
+            float a[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] += __builtin_nontemporal_load(p + (size_t)(k + u) * rows);
+            for (int u = 0; u < 8; ++u) a[u] = __builtin_nontemporal_load(p + (size_t)(k + 4 * u) * rows);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += a[u];
+        }
+        for (; k < nparts; k += 4) v += __builtin_nontemporal_load(p + (size_t)k * rows);
     }
-    for (; k < nparts; ++k) v[k % 4] += __builtin_nontemporal_load(p + (size_t)k * rows);
-    rs[row] = 1.0f / sqrtf(((v[0] + v[1]) + (v[2] + v[3])) * inv_dim + eps);
+    red[w][lane] = v;
+    __syncthreads();
+    if (w == 0 && row < rows)
+        rs[row] = 1.0f / sqrtf(((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) * inv_dim + eps);
 }
 }  // namespace
 
@@ -1282,7 +1293,7 @@ uint32_t ssd_chunked_gate_parts(const SsdArgs& a) {
 hipError_t launch_rms_from_parts(hipStream_t s, const float* part, uint32_t nparts, uint32_t rows,
                                  uint32_t dim, float eps, float* rs) {
     if (rows == 0) return hipSuccess;
-    rms_from_parts_kernel<<<(rows + 255) / 256, 256, 0, s>>>(part, nparts, rows, 1.0f / (float)dim, eps, rs);
+    rms_from_parts_kernel<<<(rows + 63) / 64, 256, 0, s>>>(part, nparts, rows, 1.0f / (float)dim, eps, rs);
     return hipGetLastError();
 }
 
