@@ -94,8 +94,8 @@ struct lssm_engine {
     bool fold_pre_norm = false;
     // batch-1 decode: in_proj, the SSD step (and out_proj) in one launch
     // (tagged words of each layer's projection and gated SSD output; the tag
-    // is a count of batch-1 steps the embedding advances, so consecutive uses
-    // of a layer's words differ by one).  Both are zeroed once at creation
+    // is a count the embedding advances on every step that uses tagged
+    // words, so consecutive uses of a word carry different tags).  Both are zeroed once at creation
     // and never reset apart.  On by default when the SSD step has work items
     // (32 state rows each) for at least half the CUs: the 2.7B shape (160
     // items) decodes at 1131 tok/s fused against 1095 in three launches, the
@@ -105,6 +105,17 @@ struct lssm_engine {
     uint64_t* xfer = nullptr;
     uint32_t* seq = nullptr;
     bool fuse_ssd = true;
+    // decode batches of 3..16 on the normalise-on-load path: the SSD step in
+    // the in_proj launch likewise (launch_inproj_ssd_decode_mma), with the
+    // rows' words in xfer_b ([n_layer][xfer_b_rows][proj]); the tag then
+    // advances on those steps too.  Bit-identical, but slower than the
+    // separate SSD step launch (2.7B batch 4: 17.6 against 8.8 + 6.7 us; batch
+    // 16: 38.8 against 9.8 + 16.1 us): one workgroup per CU keeps too little
+    // state traffic in flight, where the separate launch runs thousands of
+    // small ones.  Off by default; LSSM_FUSED_SSD_B=1 at creation turns it on.
+    uint64_t* xfer_b = nullptr;
+    uint32_t xfer_b_rows = 0;
+    bool fuse_ssd_b = false;
     // decode batches from this many rows pack x once per linear (launch_mma_pack);
     // LSSM_PACK_MIN_ROWS at creation overrides it; parts_min_rows is the same
     // for the normalise-on-load path below (LSSM_PARTS_MIN_ROWS)
@@ -223,10 +234,6 @@ struct lssm_engine {
 
     // One decode step: ids -> next (all on device).  mamba2_block.cpp:317-327.
     hipError_t decode(const int32_t* ids, uint32_t B, int32_t* next) const {
-        // the step tag advances on batch-1 steps only, the ones that use the
-        // tagged words: every use then finds the previous use's tag, minus one
-        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act, ctx->status,
-                                    fuse_ssd && B == 1 ? seq : nullptr);
         // fused RMSNorm + linear kernels: the VALU GEMV up to 4 rows, the MFMA
         // GEMV for decode batches of the shapes it takes
         const bool fused_in = (B <= 4 && (int)B <= gemv_max_rows(d_model, wfmt, act)) ||
@@ -254,6 +261,12 @@ struct lssm_engine {
         // x = r(x w) in fragment order with partial sums of squares (nopack)
         const bool frag_parts = nopack == 1 && frag_in && frag_out && parts_ok;
         const bool raw_pack = nopack == 2 && frag_in && frag_out;
+        // the batched in_proj + SSD launch (its launcher checks the rest)
+        const bool fuse_b = fuse_ssd_b && frag_parts && B >= 2 && B <= xfer_b_rows;
+        // the step tag advances on the steps that use tagged words (batch 1
+        // fused, or fuse_b): every use of a word then finds an older tag
+        hipError_t e = launch_embed(st(), embed, ids, d_hidden, B, d_model, vocab, act, ctx->status,
+                                    (fuse_ssd && B == 1) || fuse_b ? seq : nullptr);
         fused_layers = 0;
         mixer_layers = 0;
         if (e == hipSuccess) e = trace_rows(0, d_hidden, B);
@@ -308,6 +321,13 @@ struct lssm_engine {
                             a.g.nparts = 4;
                         }
                     }
+                }
+                if (!ssd_done && e == hipSuccess && fuse_b) {
+                    const SsdFuseBArgs fb{xfer_b + (size_t)li * xfer_b_rows * proj, seq, ssd_layer(li), w.A_log,
+                                          w.dt_bias, w.D, d_g, g_frag, g_part, w.mixer_norm_w, P, N, G,
+                                          DT_MIN, DT_MAX, ctx->status};
+                    ssd_done = launch_inproj_ssd_decode_mma(st(), a, fb, e);
+                    fused_layers += ssd_done ? 1u : 0u;
                 }
                 if (!ssd_done && e == hipSuccess) e = launch_inproj_decode(st(), a);
             } else {
@@ -642,6 +662,10 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     }
     const size_t xfer_bytes = (size_t)cfg->n_layer * e->xfer_words() * sizeof(uint64_t);
     A((void**)&e->xfer, xfer_bytes);
+    if (const char* v = getenv("LSSM_FUSED_SSD_B")) e->fuse_ssd_b = v[0] != '0';
+    e->xfer_b_rows = e->fuse_ssd_b && max_batch >= 3 ? std::min<uint32_t>(max_batch, 16u) : 0u;
+    const size_t xfer_b_bytes = (size_t)cfg->n_layer * e->xfer_b_rows * e->proj * sizeof(uint64_t);
+    if (xfer_b_bytes) A((void**)&e->xfer_b, xfer_b_bytes);
     A((void**)&e->seq, 256);
     // rows up to the next multiple of 16 (the GEMV's row tiles; rows past the
     // batch are read and their results dropped)
@@ -654,6 +678,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A((void**)&e->g_part, gpb);
     if (rc == LSSM_OK) {
         hipError_t err = hipMemsetAsync(e->xfer, 0, xfer_bytes, ctx->stream);
+        if (err == hipSuccess && xfer_b_bytes) err = hipMemsetAsync(e->xfer_b, 0, xfer_b_bytes, ctx->stream);
         if (err == hipSuccess) err = hipMemsetAsync(e->seq, 0, 256, ctx->stream);
         if (err == hipSuccess) err = hipMemsetAsync(e->h_frag, 0, R16 * e->d_model * es, ctx->stream);
         if (err == hipSuccess) err = hipMemsetAsync(e->g_frag, 0, R16 * d_inner * es, ctx->stream);

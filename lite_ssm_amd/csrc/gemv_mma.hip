@@ -587,6 +587,188 @@ template <typename T> struct EpiResFrag {
         part[(size_t)m * nparts + tile] = q;
     }
 };
+// Engine decode at batch 2..16 (x packed with partial sums, the single-pass
+// kernel): the in_proj rows of EpiInproj published as tagged words,
+// xfer[m proj + n] = value bits | step tag << 32 (the batch-1 launch's
+// scheme, gemv.hip), then the SSD step + SiLU(z) gate of the items (row m,
+// 32 consecutive rows j = h P + p of the flattened (H, P)) blockIdx.x,
+// blockIdx.x + grid, ... in the same launch, with ssd_step_kernel<FRAG>'s
+// arithmetic and outputs (ssd_step.metal:33-77): y, r(y w) in out_proj's
+// fragment order and the 32 values' sum of squares of y.  An item waits for
+// its 2N + 65 words (B and C of the group, x and z of its rows, dt of the
+// head), which other blocks of the launch store; the launcher takes grids of
+// at most one block per CU, so every block is resident and every awaited word
+// gets written.  The wait is bounded all the same: an item whose words do not
+// all arrive leaves its state as it was, writes NaN and sets
+// STATUS_WAIT_TIMEOUT in the context's status word.
+template <typename T> struct EpiInprojSsdB {
+    static constexpr bool kTail = true;
+    static constexpr uint32_t IP = 32;                    // state rows per item
+    static constexpr uint32_t NV = 8;                     // lanes per state row
+    static constexpr uint32_t NN = 128;                   // d_state
+    static constexpr int F = (int)(NN / (4 * NV));        // 16-byte state pieces per lane
+    static constexpr uint32_t NWD = 2 * NN + 2 * IP + 1;  // words an item reads
+    static constexpr uint32_t SPIN = 1u << 16;            // polls before giving up
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    EpiInproj<T> in;                                      // routing / conv (its z, xbc_act, dt unused)
+    uint64_t* xfer;                                       // [M][proj] tagged words of this layer
+    uint32_t proj;
+    const uint32_t* seq;                                  // the step tag (device)
+    float* state;                                         // [M][H][P][NN] of this layer
+    const T* A_log;
+    const T* dt_bias;
+    const T* D;                                           // nullptr: no D term
+    T* y;                                                 // [M][d_inner]
+    T* yfrag;                                             // r(y w), out_proj's fragment order
+    float* ypart;                                         // [M][H P / IP] sums of y^2
+    const T* ynorm_w;                                     // out_proj's norm weight
+    uint32_t P, G, M;
+    float dt_min, dt_max;
+    uint32_t* status;
+    uint32_t wait_skew;                                   // 0; 1 = wait for a tag nobody publishes
+    using Pre = typename EpiInproj<T>::Pre;
+    __device__ __forceinline__ void pin() const {
+        in.pin();
+        pin_arg(xfer);
+        pin_arg(proj);
+        pin_arg(seq);
+    }
+    __device__ __forceinline__ Pre prefetch(int m, uint32_t n) const { return in.prefetch(m, n); }
+    __device__ __forceinline__ void operator()(int m, uint32_t n, float acc, const Pre& p) const {
+        const T v = in.value(m, n, acc, p);
+        const uint64_t word = (uint64_t)bits16(v) | ((uint64_t)*seq << 32);
+        __hip_atomic_store(xfer + (size_t)m * proj + n, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    static constexpr int GI = 4;                          // items a block takes at once
+    // The state slice of item `it` (every thread loads: threads past the
+    // item's 256 take row 0's, unused)
+    __device__ __forceinline__ void load_state(uint32_t it, f32x4 (&s)[F]) const {
+        const uint32_t H = in.H, ipr = H * P / IP, b = it / ipr, j0 = (it % ipr) * IP;
+        const uint32_t t = threadIdx.x, pl = t < IP * NV ? t / NV : 0, j = j0 + pl;
+        const f32x4* S = reinterpret_cast<const f32x4*>(state + (((size_t)b * H + j / P) * P + j % P) * NN);
+#pragma unroll
+        for (int f = 0; f < F; ++f) s[f] = __builtin_nontemporal_load(&S[t % NV + NV * f]);   // streamed once
+    }
+    // Word u of item `it`'s NWD words: its index in the row's projection.
+    __device__ __forceinline__ uint32_t word_idx(uint32_t it, uint32_t u) const {
+        const uint32_t d_inner = in.d_inner, H = in.H, GN = G * NN;
+        const uint32_t ipr = H * P / IP, j0 = (it % ipr) * IP, h = j0 / P, g = h / (H / G);
+        if (u < NN) return 2 * d_inner + g * NN + u;                                  // B
+        if (u < 2 * NN) return 2 * d_inner + GN + g * NN + (u - NN);                  // C
+        if (u < 2 * NN + IP) return d_inner + j0 + (u - 2 * NN);                      // x
+        if (u < 2 * NN + 2 * IP) return j0 + (u - 2 * NN - IP);                       // z
+        return d_inner + in.xbc + h;                                                  // dt
+    }
+    // The step of item `it` (slot d of the group) from its state slice and
+    // its words in wv[d]; q: this thread's share of the 32 rows' sum of y^2.
+    __device__ __forceinline__ float step(uint32_t it, const f32x4 (&s)[F], const uint32_t* wv,
+                                          bool timed_out) const {
+        const uint32_t d_inner = in.d_inner, H = in.H;
+        const uint32_t ipr = H * P / IP, b = it / ipr, j0 = (it % ipr) * IP, h = j0 / P;
+        const uint32_t t = threadIdx.x, lr = t % NV, pl = t / NV, j = j0 + pl, p = j % P;
+        f32x4* S = reinterpret_cast<f32x4*>(state + (((size_t)b * H + h) * P + p) * NN);
+        const float xv = f_of_raw<T>(wv[2 * NN + pl]);
+        const float A_h = -expf(f_of_raw<T>(raw_at(A_log + h)));
+        float dt = softplus_f(f_of_raw<T>(wv[2 * NN + 2 * IP]) + f_of_raw<T>(raw_at(dt_bias + h)));
+        dt = fminf(fmaxf(dt, dt_min), dt_max);
+        const float decay = expf(A_h * dt);
+        float ys = 0.0f;
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+            const uint32_t n0 = 4 * (lr + NV * f);
+            const float b0 = f_of_raw<T>(wv[n0]), b1 = f_of_raw<T>(wv[n0 + 1]);
+            const float b2 = f_of_raw<T>(wv[n0 + 2]), b3 = f_of_raw<T>(wv[n0 + 3]);
+            const float c0 = f_of_raw<T>(wv[NN + n0]), c1 = f_of_raw<T>(wv[NN + n0 + 1]);
+            const float c2 = f_of_raw<T>(wv[NN + n0 + 2]), c3 = f_of_raw<T>(wv[NN + n0 + 3]);
+            // the same fused multiply-adds as ssd_step_kernel
+            f32x4 tt = s[f];
+            tt.x = fmaf(decay, tt.x, dt * b0 * xv);
+            tt.y = fmaf(decay, tt.y, dt * b1 * xv);
+            tt.z = fmaf(decay, tt.z, dt * b2 * xv);
+            tt.w = fmaf(decay, tt.w, dt * b3 * xv);
+            if (!timed_out) __builtin_nontemporal_store(tt, &S[lr + NV * f]);
+            ys += fmaf(c3, tt.w, fmaf(c2, tt.z, fmaf(c0, tt.x, c1 * tt.y)));
+        }
+        ys = group_sum<NV>(ys);
+        float q = 0.0f;
+        if (lr == 0) {
+            const float dv = D ? f_of_raw<T>(raw_at(D + h)) : 0.0f;
+            float yv = rnd<T>(fmaf(dv, xv, ys));
+            yv = silu_fast(f_of_raw<T>(wv[2 * NN + IP + pl])) * yv;
+            const T yr = from_f<T>(yv);
+            y[(size_t)b * d_inner + j] = yr;
+            const float yf = to_f(yr);
+            yfrag[frag_half(b, j, H * P / 128)] = from_f<T>(yf * f_of_raw<T>(raw_at(ynorm_w + j)));
+            q = yf * yf;
+        }
+        // the wave's 8 rows (lanes 8 i)
+        q += __shfl_xor(q, 8);
+        q += __shfl_xor(q, 16);
+        q += __shfl_xor(q, 32);
+        return q;
+    }
+    __device__ __forceinline__ uint32_t mine() const {
+        const uint32_t items = M * (in.H * P / IP), gs = gridDim.x;
+        return blockIdx.x < items ? (items - blockIdx.x + gs - 1) / gs : 0u;
+    }
+    // Items k0 .. k0 + GI - 1 of the block (b + k grid), state in st: all
+    // their words awaited together (one round trip to the other workgroups'
+    // stores per group, not per item), then the steps.  Threads 256..
+    // (blocks of more than four waves) take part in the waits and barriers only.
+    __device__ __forceinline__ void group(uint32_t k0, uint32_t n, const f32x4 (&st)[GI][F], uint32_t tag) const {
+        __shared__ uint32_t wv[GI][NWD];                  // B, C, x, z, dt value bits
+        __shared__ float red[GI][4];
+        constexpr uint32_t QNAN = __is_same(T, f16) ? 0x7E00u : 0x7FC0u;
+        const uint32_t ipr = in.H * P / IP, gs = gridDim.x, t = threadIdx.x;
+        __syncthreads();                                  // the previous group's words and sums read
+        int late = 0;                                     // a word of this thread never arrived
+        for (uint32_t v = t; v < n * NWD; v += blockDim.x) {
+            const uint32_t d = v / NWD, u = v % NWD, it = blockIdx.x + (k0 + d) * gs;
+            const uint64_t* wp = xfer + (size_t)(it / ipr) * proj + word_idx(it, u);
+            uint64_t w = __hip_atomic_load(wp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t c = 0; (uint32_t)(w >> 32) != tag && c < SPIN; ++c)
+                w = __hip_atomic_load(wp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            late |= (uint32_t)(w >> 32) != tag;
+            wv[d][u] = (uint32_t)(w >> 32) == tag ? (uint32_t)w : QNAN;
+        }
+        // the state slices are stored only when every word of the group arrived
+        const bool timed_out = __syncthreads_or(late) != 0;
+        if (timed_out && t == 0) atomicOr(status, STATUS_WAIT_TIMEOUT);
+#pragma unroll
+        for (int d = 0; d < GI; ++d) {
+            if ((uint32_t)d < n && t < IP * NV) {
+                const float q = step(blockIdx.x + (k0 + d) * gs, st[d], wv[d], timed_out);
+                if (t % WAVE == 0) red[d][t / WAVE] = q;
+            }
+        }
+        __syncthreads();
+        // the 4 waves' sums of each item in order (ssd_step_kernel's)
+        if (t < n) {
+            const uint32_t it = blockIdx.x + (k0 + t) * gs;
+            ypart[(size_t)(it / ipr) * ipr + it % ipr] = red[t][0] + red[t][1] + red[t][2] + red[t][3];
+        }
+    }
+    // The block's items b, b + grid, ... in groups of GI, each group's state
+    // slices requested before its words are awaited.
+    __device__ __forceinline__ void tail() const {
+        const uint32_t tag = *seq + wait_skew, n = mine(), gs = gridDim.x;
+        for (uint32_t k0 = 0; k0 < n; k0 += GI) {
+            const uint32_t c = min((uint32_t)GI, n - k0);
+            f32x4 st[GI][F];
+#pragma unroll
+            for (int d = 0; d < GI; ++d)
+                if ((uint32_t)d < c) load_state(blockIdx.x + (k0 + d) * gs, st[d]);
+            group(k0, c, st, tag);
+        }
+    }
+};
+template <class E, class = void> struct epi_tail {
+    static constexpr bool value = false;
+};
+template <class E> struct epi_tail<E, decltype((void)E::kTail)> {
+    static constexpr bool value = E::kTail;
+};
+
 template <class E, class = void> struct epi_parts {
     static constexpr bool value = false;
 };
@@ -841,6 +1023,7 @@ __global__ __launch_bounds__(64 * MMX_MAXW) void gemv_mmx_kernel(GemvCore c, Epi
             }
         }
     }
+    if constexpr (epi_tail<Epi>::value) epi.tail();
 }
 
 // LSSM_MMA_STAGED=1 (read once) keeps packed x on the staging kernel, for A/B
@@ -1261,6 +1444,35 @@ bool launch_gemv_mma(hipStream_t s, const GemvArgs& a, hipError_t& err) {
     if (a.act == LSSM_F16) return go(f16{});
     if (a.act == LSSM_BF16) return go(bf16{});
     return false;
+}
+
+bool launch_inproj_ssd_decode_mma(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseBArgs& f,
+                                  hipError_t& err) {
+    const GemvArgs& g = a.g;
+    if (g.act != LSSM_BF16 || g.wfmt != LSSM_W_Q4_G64 || !g.xpack || !g.xpart || !g.norm_w) return false;
+    if (g.M < 2 || g.M > 16 || g.M < mma_min_rows() || mmx_disabled()) return false;
+    if (f.N != 128 || f.P == 0 || f.P % 32 != 0 || f.G == 0 || a.H % f.G != 0 || (a.H * f.P) % 128 != 0 ||
+        a.d_inner != a.H * f.P || a.xbc != a.d_inner + 2 * f.G * f.N || g.N != a.d_inner + a.xbc + a.H)
+        return false;
+    if (!f.xfer || !f.seq || !f.state || !f.y || !f.yfrag || !f.ypart || !f.ynorm_w || !f.status) return false;
+    GemvCore c{g.x, g.x_stride, (const uint8_t*)g.w, (const uint16_t*)g.s, g.norm_w, g.eps, g.N, g.K, 1.0f / (float)g.K};
+    c.xp = static_cast<const uint32_t*>(g.xpack);
+    c.part = g.xpart;
+    c.nparts = g.nparts;
+    if (!mma_aligned<bf16>(c, true)) return false;
+    MmxPlan q;
+    if (!mmx_plan<LSSM_W_Q4_G64, bf16>(g.M, g.N, g.K, q)) return false;
+    // every block resident at once (one per CU at most), four waves an item
+    const uint32_t blocks = ((g.N + 15) / 16 + q.ct - 1) / q.ct;
+    if (blocks > num_cus() || q.ks * WAVE < 256) return false;
+    using T = bf16;
+    EpiInprojSsdB<T> e{EpiInproj<T>{a.d_inner, a.xbc, a.H, a.dconv, (T*)a.conv_state, (const T*)a.conv_w,
+                                    (const T*)a.conv_b, nullptr, nullptr, nullptr},
+                       f.xfer, g.N, f.seq, f.state, (const T*)f.A_log, (const T*)f.dt_bias, (const T*)f.D,
+                       (T*)f.y, (T*)f.yfrag, f.ypart, (const T*)f.ynorm_w, f.P, f.G, g.M, f.dt_min, f.dt_max,
+                       f.status, f.wait_skew};
+    err = mmx_go<LSSM_W_Q4_G64, T>(s, c, e, g.M, q);
+    return true;
 }
 
 bool launch_inproj_decode_mma(hipStream_t s, const InprojDecodeArgs& a, hipError_t& err) {

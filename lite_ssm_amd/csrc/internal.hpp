@@ -341,6 +341,30 @@ bool launch_layer_decode(hipStream_t s, const InprojDecodeArgs& a, const SsdFuse
 // shape, format or alignment is not one it takes; err holds the launch result.
 bool launch_gemv_mma(hipStream_t s, const GemvArgs& a, hipError_t& err);
 bool launch_inproj_decode_mma(hipStream_t s, const InprojDecodeArgs& a, hipError_t& err);
+// Engine decode at batch 2..16 with x packed in fragment order with partial
+// sums (a.g.xpack, a.g.xpart): launch_inproj_decode_mma's rows published as
+// tagged words, then the layer's SSD step + SiLU(z) gate with the outputs of
+// launch_ssd_step's fragment variant (y, r(y ynorm_w) in yfrag, sums of y^2 in
+// ypart), in one launch; z / xbc_act / dt of `a` are not written.  Returns
+// false (launching nothing) for shapes, formats or grids it does not take.
+struct SsdFuseBArgs {
+    uint64_t* xfer;          // [M][proj] tagged words of this layer (zeroed once)
+    const uint32_t* seq;     // step tag in device memory, advanced once per decode step
+    float* state;            // [M][H][P][N] fp32
+    const void* A_log;
+    const void* dt_bias;
+    const void* D;           // may be null
+    void* y;                 // [M][d_inner]
+    void* yfrag;             // r(y ynorm_w) in the single-pass GEMV's fragment order
+    float* ypart;            // [M][H P / 32]
+    const void* ynorm_w;
+    uint32_t P, N, G;
+    float dt_min, dt_max;
+    uint32_t* status;        // STATUS_WAIT_TIMEOUT when a wait gives up
+    uint32_t wait_skew = 0;  // 1: wait for a tag that is never published
+};
+bool launch_inproj_ssd_decode_mma(hipStream_t s, const InprojDecodeArgs& a, const SsdFuseBArgs& f,
+                                  hipError_t& err);
 // Whether a decode batch of M rows runs in one MFMA launch (16-byte aligned
 // operands assumed; otherwise the launchers fall back to gemv1 launches).
 bool gemv_mma_takes(uint32_t M, uint32_t N, uint32_t K, int wfmt, int act);

@@ -498,6 +498,64 @@ def test_engine_fused_ssd_decode_bs1(ctx, tag, name, act, wfmt, over, mixer):
         plain.close()
 
 
+def test_engine_fused_ssd_decode_batched(ctx, monkeypatch):
+    """Decode batches of 3..16 (the normalise-on-load path) with the SSD step
+    inside the single-pass MFMA in_proj launch (tagged words per row):
+    bit-identical to the separate SSD step launch (LSSM_FUSED_SSD_B=0) in
+    logits, conv and SSD state and the ids, on every step, eager and
+    graph-replayed, with the batch changing between calls (stale words of
+    larger batches must not be taken); within tolerance of the oracle.  Batch
+    2 takes the VALU GEMV and is not fused."""
+    from lite_ssm_amd.model import Engine
+    L, sh, m, om = _setup(ctx, "mamba2-2.7b", O.BF16, O.W_Q4_G64, n_layer=2, vocab_size=512, seed=41)
+    Lq, BMAX = 6, 16
+    monkeypatch.setenv("LSSM_FUSED_SSD_B", "1")
+    fused = Engine(ctx, m, max_batch=BMAX, max_seq=Lq)
+    monkeypatch.setenv("LSSM_FUSED_SSD_B", "0")
+    plain = Engine(ctx, m, max_batch=BMAX, max_seq=Lq)
+    try:
+        for B in (16, 4, 3, 2, 8):
+            print(f"case: batched fused SSD, batch {B}", flush=True)
+            ids = np.random.default_rng(B).integers(0, sh.vocab_size, (B, Lq)).astype(np.int32)
+            n_f = torch.zeros(B, dtype=torch.int32, device="cuda")
+            n_p = torch.zeros_like(n_f)
+            fused.reset()
+            plain.reset()
+            fused.prefill(torch.from_numpy(ids).cuda(), n_f)
+            plain.prefill(torch.from_numpy(ids).cuda(), n_p)
+            conv, ssd = om.new_state(B)
+            ref = om.prefill(conv, ssd, ids)
+            tok = O.argmax(ref, O.BF16)
+
+            def same(step):
+                assert torch.equal(fused.logits(B), plain.logits(B)), f"batch {B} logits, step {step}"
+                cf, sf = fused.state()
+                cp, sp = plain.state()
+                assert torch.equal(sf[:, :B], sp[:, :B]) and torch.equal(cf[:, :B], cp[:, :B]), \
+                    f"batch {B} state, step {step}"
+
+            want = (sh.n_layer, 0) if B >= 3 else (0, 0)
+            for step in range(3):
+                t = torch.from_numpy(tok).cuda()
+                fused.decode(t, n_f)
+                plain.decode(t, n_p)
+                assert fused.fused_layers() == want and plain.fused_layers() == (0, 0), f"batch {B}"
+                same(step)
+                ref = om.decode(conv, ssd, tok)
+                _check_logits(fused.logits(B).float().cpu().numpy(), ref, O.BF16, f"batch {B} decode {step}")
+                tok = O.argmax(ref, O.BF16)
+            t_f = torch.from_numpy(tok).cuda()
+            t_p = t_f.clone()
+            fused.decode_graph(t_f, t_f, 5)
+            for _ in range(5):
+                plain.decode(t_p, t_p)
+            assert torch.equal(t_f, t_p), f"batch {B} graph ids"
+            same("graph")
+    finally:
+        fused.close()
+        plain.close()
+
+
 def test_engine_default_bs1_fuses_ssd_only(ctx):
     """The default batch-1 decode runs the SSD step inside the in_proj launch
     and out_proj as its own launch (LSSM_FUSED_MIXER unset), bit-identical to
