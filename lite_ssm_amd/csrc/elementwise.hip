@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void conv1d_vec_kernel(const T* __restrict__ x
         for (int c = 0; c < 8; ++c) {
             float acc = bf[c];
 #pragma unroll
-            for (int tap = 0; tap < 4; ++tap) acc += wf[c][tap] * el8<T>(win[i + tap], c);
+            for (int tap = 0; tap < 4; ++tap) acc = fmaf(wf[c][tap], el8<T>(win[i + tap], c), acc);
             o[c] = rnd<T>(acc);
             if (SILU) o[c] = silu_fast(o[c]);
         }
