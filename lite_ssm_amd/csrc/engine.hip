@@ -430,11 +430,11 @@ struct lssm_engine {
                 sg.z = projb;                                  // z: columns 0 .. d_inner of the projection
                 sg.z_stride = proj;
                 sg.gnorm_w = w.mixer_norm_w;
+                sg.z_silu = true;                              // in_proj stores r(silu(z)) (silu_cols)
                 gparts = ssd_chunked_gate_parts(sg);
                 if (gparts) {
                     s = sg;
                     s.gpart = gpart;
-                    s.z_silu = true;
                 }
             }
             if (e == hipSuccess && !fused) {

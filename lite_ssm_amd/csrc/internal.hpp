@@ -250,8 +250,8 @@ struct SsdArgs {
     // the 1 / rms scale is then applied by the GEMM that reads Y
     const void* gnorm_w = nullptr;
     float* gpart = nullptr;
-    // with gpart: z already holds r(silu(z)) (the projection's GEMM applied
-    // it), so g = r(z r(y))
+    // z already holds r(silu(z)) (the projection's GEMM applied it), so
+    // g = r(z r(y)); the fused gate is taken only then
     bool z_silu = false;
 };
 hipError_t launch_ssd_step(hipStream_t s, const SsdArgs& a);

@@ -790,13 +790,13 @@ void ssd_chunk_mfma_kernel(SsdArgs a) {
             if (gate) {
                 // the gated RMSNorm's front half (gated_rmsnorm: g =
                 // r(silu(z) r(y)), then g w): r(g w) stored, sum of g^2 kept
-                // (z_silu: the projection GEMM stored r(silu(z)) already)
+                // (the projection GEMM stored r(silu(z)) as z)
                 const floatx4 zf = unpack4<T>(__builtin_bit_cast(s4v, zr[Tt]));
                 floatx4 o;
                 float sq = 0.0f;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float g = rnd<T>((a.z_silu ? zf[r] : silu_fast(zf[r])) * rnd<T>(yacc[Tt][r]));
+                    const float g = rnd<T>(zf[r] * rnd<T>(yacc[Tt][r]));
                     o[r] = g * gw[r];
                     sq = fmaf(g, g, sq);
                 }
@@ -1283,7 +1283,7 @@ __global__ __launch_bounds__(256) void rms_from_parts_kernel(const float* __rest
 }  // namespace
 
 uint32_t ssd_chunked_gate_parts(const SsdArgs& a) {
-    if (a.batch == 0 || a.H == 0 || a.L == 0 || !mfma_ok(a)) return 0;
+    if (a.batch == 0 || a.H == 0 || a.L == 0 || !mfma_ok(a) || !a.z_silu) return 0;
     if (!a.z || !a.gnorm_w || a.z_stride % 4 != 0 || (uintptr_t)a.z % 8 != 0 ||
         (uintptr_t)a.gnorm_w % 8 != 0)
         return 0;
