@@ -744,11 +744,21 @@ def test_embed_and_argmax(ctx, rng, act):
                              vocab, act))
     assert np.array_equal(act_host(out, act), table[ids])
     lg = O.to_act(rng.standard_normal((3, vocab)), act)
-    lg[1, 777] = lg[1, 40000] = O.to_act(np.array([99.0]), act)[0]      # tie -> first index
+    top = O.to_act(np.array([99.0]), act)[0]
+    lg[1, 777] = lg[1, 40000] = top                                    # tie -> first index
+    lg[2, 8 * 3000 + 5] = lg[2, 8 * 3000 + 2] = lg[2, 8 * 4100 + 1] = top  # within one 8-value piece, and across threads
     got = torch.zeros(3, dtype=torch.int32, device="cuda")
     L.check(L.lib.lssm_argmax(ctx.h, dev(lg).data_ptr(), got.data_ptr(), 3, vocab, act))
     assert list(host(got, np.int32)) == list(O.argmax(lg, act))
-    assert host(got, np.int32)[1] == 777
+    assert host(got, np.int32)[1] == 777 and host(got, np.int32)[2] == 8 * 3000 + 2
+    # an odd vocabulary (the two-stage path) and a longer one (more than one pass of a block)
+    for v, rows in ((50277, 2), (256000, 1), (65536, 4)):
+        lg2 = O.to_act(rng.standard_normal((rows, v)), act)
+        lg2[rows - 1, v - 1] = top
+        got2 = torch.zeros(rows, dtype=torch.int32, device="cuda")
+        L.check(L.lib.lssm_argmax(ctx.h, dev(lg2).data_ptr(), got2.data_ptr(), rows, v, act))
+        assert list(host(got2, np.int32)) == list(O.argmax(lg2, act)), f"vocab {v}"
+        assert host(got2, np.int32)[rows - 1] == v - 1
 
 
 def test_batch_lifecycle_errors(ctx):
