@@ -250,39 +250,54 @@ template <typename T> __device__ __forceinline__ uint32_t pk2(float lo, float hi
     }
 }
 
-// r(q s) for 16 weights -> 8 packed pairs.  int4: the unsigned nibble
-// u = q + 8 is placed by v_perm into the mantissa of the fp32 128 + u, and
-// fma(128 + u, s, -136 s) = q s exactly (-136 s is exact: 8 + 11 bits); int8:
-// u = q + 128 as a float and fma(u, s, -128 s).  One rounding, at the pack.
+// r(q s) for 8 consecutive weights -> 4 packed pairs (k order).  The
+// unsigned value u (int4: q + 8, int8: q + 128) of two weights is placed by
+// one v_perm into the mantissas of two fp16 values 1024 + u (bits
+// 0x6400 | u), and fma(1024 + u, s, c) with c = -(1024 + 8) s (int8:
+// -(1024 + 128) s) is q s exactly: both products have at most 11 + 11
+// significant bits and q s at most 15, all exact in fp32; the fp16 operands
+// convert inside v_fma_mix_f32.  One rounding, at the pack.  int4: q0 holds
+// the 8 nibbles (k = nibble index); int8: q0, q1 the 8 bytes.
+template <int FMT, typename T>
+__device__ __forceinline__ u32x4 dequant8(uint32_t q0, uint32_t q1, float s, float c) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    // bytes (b0 of v, 0x64, b1 of v, 0x64) and (b2, 0x64, b3, 0x64)
+    auto pair01 = [](uint32_t v) { return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u)); };
+    auto pair23 = [](uint32_t v) { return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)); };
+    auto f = [&](_Float16 e) { return __builtin_fmaf((float)e, s, c); };
+    if constexpr (FMT == LSSM_W_Q8_G32) {
+        const uint32_t d0 = q0 ^ 0x80808080u, d1 = q1 ^ 0x80808080u;
+        const h2 a = pair01(d0), b = pair23(d0), e = pair01(d1), g = pair23(d1);
+        return u32x4{pk2<T>(f(a.x), f(a.y)), pk2<T>(f(b.x), f(b.y)), pk2<T>(f(e.x), f(e.y)), pk2<T>(f(g.x), f(g.y))};
+    } else {
+        // u of k 0, 2, 4, 6 (low nibbles) and k 1, 3, 5, 7
+        const uint32_t lo = (q0 & 0x0F0F0F0Fu) ^ 0x08080808u;
+        const uint32_t hi = ((q0 >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+        const h2 e02 = pair01(lo), e46 = pair23(lo), e13 = pair01(hi), e57 = pair23(hi);
+        return u32x4{pk2<T>(f(e02.x), f(e13.x)), pk2<T>(f(e02.y), f(e13.y)),
+                     pk2<T>(f(e46.x), f(e57.x)), pk2<T>(f(e46.y), f(e57.y))};
+    }
+}
+template <int FMT> __device__ __forceinline__ float dequant_bias(float s) {
+    return (FMT == LSSM_W_Q8_G32 ? -1152.0f : -1032.0f) * s;
+}
+
+// 16 weights -> 8 packed pairs
 template <int FMT, typename T>
 __device__ __forceinline__ void dequant16(const WRaw<FMT>& r, uint32_t out[8]) {
-    const float s = fp16_bits_to_f((uint16_t)r.s);
+    const float s = fp16_bits_to_f((uint16_t)r.s), c = dequant_bias<FMT>(s);
+    u32x4 a, b;
     if constexpr (FMT == LSSM_W_Q8_G32) {
-        const float c = -128.0f * s;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t d = r.q[i] ^ 0x80808080u;
-            // (byte -> float converts to v_cvt_f32_ubyte{0..3})
-            const float f0 = (float)(d & 0xFFu), f1 = (float)((d >> 8) & 0xFFu);
-            const float f2 = (float)((d >> 16) & 0xFFu), f3 = (float)(d >> 24);
-            out[2 * i] = pk2<T>(__builtin_fmaf(f0, s, c), __builtin_fmaf(f1, s, c));
-            out[2 * i + 1] = pk2<T>(__builtin_fmaf(f2, s, c), __builtin_fmaf(f3, s, c));
-        }
+        a = dequant8<FMT, T>(r.q[0], r.q[1], s, c);
+        b = dequant8<FMT, T>(r.q[2], r.q[3], s, c);
     } else {
-        const float c = -136.0f * s;
+        a = dequant8<FMT, T>(r.q[0], 0u, s, c);
+        b = dequant8<FMT, T>(r.q[1], 0u, s, c);
+    }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t d = r.q[i] ^ 0x88888888u;
-            const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
-            // element 2b is byte b of lo, element 2b + 1 byte b of hi
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const uint32_t sel = 0x04000C0Cu | ((uint32_t)b << 16);
-                const float e0 = __uint_as_float(__builtin_amdgcn_perm(0x43434343u, lo, sel));
-                const float e1 = __uint_as_float(__builtin_amdgcn_perm(0x43434343u, hi, sel));
-                out[4 * i + b] = pk2<T>(__builtin_fmaf(e0, s, c), __builtin_fmaf(e1, s, c));
-            }
-        }
+    for (int i = 0; i < 4; ++i) {
+        out[i] = a[i];
+        out[4 + i] = b[i];
     }
 }
 
