@@ -137,6 +137,15 @@ __device__ __forceinline__ size_t frag_half(uint32_t m, uint32_t k, uint32_t qua
 // Sum over a full 64-lane wave; result in every lane.
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<WAVE>(v); }
 
+// sampler.cpp:13-21: first index of the maximum.  (v, i) beats (v', i') iff
+// v > v' or (v == v' and i < i'); a NaN never wins.
+__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
 // Block-wide sum for blockDim.x == NT threads; `red` is >= NT/64 floats of LDS.
 template <int NT> __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);

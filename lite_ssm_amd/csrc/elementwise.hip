@@ -370,15 +370,6 @@ __global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restr
     }
 }
 
-// sampler.cpp:13-21: first index of the maximum.  (v, i) beats (v', i') iff
-// v > v' or (v == v' and i < i').
-__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
-}
-
 template <int NTHR>
 __device__ __forceinline__ void block_argmax(float& bv, int& bi) {
     __shared__ float sv[NTHR / WAVE];
@@ -426,9 +417,13 @@ __global__ __launch_bounds__(NTHR) void argmax_partial_kernel(const T* __restric
     }
 }
 
+// nblk_dev (optional): the partial count, written by the kernel before (the
+// lm_head GEMV's argmax epilogue writes one partial per block of its grid).
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float* pv, const int* pi,
-                                                           uint32_t nblk, int32_t* ids) {
+                                                           uint32_t nblk, const uint32_t* nblk_dev,
+                                                           int32_t* ids) {
     const uint32_t row = blockIdx.x;
+    if (nblk_dev) nblk = *nblk_dev;
     float bv = -FLT_MAX;
     int bi = 0x7fffffff;
     for (uint32_t i = threadIdx.x; i < nblk; i += 256)
@@ -649,7 +644,13 @@ hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32
     LSSM_DISPATCH_ACT(act, T,
                       argmax_partial_kernel<T, 256><<<dim3(nblk, rows), 256, 0, s>>>(
                           (const T*)logits, vocab, pv, pi, ids));
-    argmax_final_kernel<<<rows, 256, 0, s>>>(pv, pi, nblk, ids);
+    argmax_final_kernel<<<rows, 256, 0, s>>>(pv, pi, nblk, nullptr, ids);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_final(hipStream_t s, const float* pv, const int* pi, const uint32_t* nblk,
+                               int32_t* ids) {
+    argmax_final_kernel<<<1, 256, 0, s>>>(pv, pi, 0u, nblk, ids);
     return hipGetLastError();
 }
 

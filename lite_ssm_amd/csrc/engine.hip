@@ -70,6 +70,10 @@ struct lssm_engine {
     void* conv_state = nullptr;
     float* ssd_state = nullptr;
     void* argmax_scratch = nullptr;
+    size_t argmax_scratch_bytes = 0;
+    // batch-1 greedy id from the lm_head launch's per-block partials
+    // (LSSM_FUSED_ARGMAX=0: the two-pass argmax over the stored logits)
+    bool fuse_argmax = true;
     float* gram = nullptr;     // prefill: the chunks' C B^T tiles, shared by a group's heads
     float* seg = nullptr;      // prefill: the chunked scan's segment workspace
     // prefill: the split-K slices of GEMMs whose grid leaves most CUs idle
@@ -221,6 +225,11 @@ struct lssm_engine {
         if (rows <= 4 && gemv_max_rows(d_model, LSSM_W_DENSE, act) >= 1) {
             GemvArgs g{x, xs, lm_head, nullptr, logits, vocab, nullptr, norm_f, RMS_EPS, rows, vocab,
                        d_model, LSSM_W_DENSE, act, LSSM_EPI_NONE};
+            // one row: the argmax's first pass folded into the lm_head launch
+            if (rows == 1 && fuse_argmax) {
+                e = launch_gemv_argmax(st(), g, next, argmax_scratch, argmax_scratch_bytes);
+                if (e != hipErrorNotSupported) return e;
+            }
             e = launch_gemv(st(), g);
         } else {
             e = launch_rmsnorm(st(), x, xs, norm_f, d_normed, d_model, rows, d_model, RMS_EPS, act);
@@ -643,7 +652,10 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A(&e->logits, (size_t)max_batch * e->vocab * es);
     A(&e->conv_state, (size_t)cfg->n_layer * max_batch * e->xbc * e->K * es);
     A((void**)&e->ssd_state, (size_t)cfg->n_layer * max_batch * e->H * e->P * e->N * sizeof(float));
-    A(&e->argmax_scratch, (size_t)max_batch * 128 * 8);
+    // the two-pass argmax: 128 partials per row; the lm_head's fused first
+    // pass: a count and up to 1024 partials
+    e->argmax_scratch_bytes = std::max((size_t)max_batch * 128 * 8, (size_t)16 + 1024 * 8);
+    A(&e->argmax_scratch, e->argmax_scratch_bytes);
     A((void**)&e->gram, ssd_gram_floats(max_batch, max_seq, G) * sizeof(float));
     A((void**)&e->seg, ssd_seg_floats() * sizeof(float));
     A((void**)&e->gemm_ws, GEMM_WS_FLOATS * sizeof(float));
@@ -695,6 +707,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     if (const char* v = getenv("LSSM_NOPACK")) e->nopack = (int)strtol(v, nullptr, 10);
     if (const char* v = getenv("LSSM_FUSED_GATED_NORM")) e->fuse_gated_norm = v[0] != '0';
     if (const char* v = getenv("LSSM_FOLD_PRE_NORM")) e->fold_pre_norm = v[0] != '0';
+    if (const char* v = getenv("LSSM_FUSED_ARGMAX")) e->fuse_argmax = v[0] != '0';
     if (rc != LSSM_OK) {
         delete e;
         return rc;

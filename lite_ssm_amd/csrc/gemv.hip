@@ -29,6 +29,7 @@
 //  * gemv_lds (any dtype, any alignment): x rows staged once per block in LDS
 //    as fp32, padded by 4 floats per chunk so that the 16-byte reads of the 16
 //    lanes of a row fall in distinct banks; 16 lanes per row.
+#include <cfloat>
 #include <type_traits>
 
 #include "gemv_core.hpp"
@@ -451,6 +452,65 @@ template <class Epi, bool = Epi::kTail> struct EarlyOf {
 };
 template <class Epi> struct EarlyOf<Epi, true> {
     using type = typename Epi::Early;
+};
+
+// The lm_head of a batch-1 decode step with its greedy id (sampler.cpp:13-21):
+// y[n] = r(acc) as EpiPlain stores it, and the lane that stores a row keeps
+// the best (r(acc), n) of its rows by argmax_merge on the stored value; after
+// the rows the block reduces them and writes its partial (pv, pi)[blockIdx.x],
+// block 0 also the partial count (the grid size) to *count.  A reduction of
+// the partials in any order gives the first index of the maximum, as
+// argmax_partial_kernel over the stored logits does.  Nothing waits on other
+// blocks.
+template <typename T> struct EpiLogitsArgmax {
+    static constexpr bool kNormOptional = true;
+    static constexpr bool kTail = true;
+    T* y;
+    float* pv;
+    int* pi;
+    uint32_t* count;
+    mutable float bv = -FLT_MAX;
+    mutable int bi = 0x7fffffff;
+    struct Pre {};
+    struct Early {};
+    bool fits(uint32_t bd) const { return bd % WAVE == 0 && bd / WAVE <= 16; }
+    __device__ __forceinline__ void pin() const {
+        pin_arg(y);
+        pin_arg(pv);
+        pin_arg(pi);
+        pin_arg(count);
+    }
+    __device__ __forceinline__ Pre prefetch(int, uint32_t) const { return Pre{}; }
+    __device__ __forceinline__ void operator()(int, uint32_t n, float acc, const Pre&) const {
+        const T r = from_f<T>(acc);
+        y[n] = r;
+        argmax_merge(bv, bi, to_f(r), (int)n);
+    }
+    __device__ __forceinline__ void early(Early&) const {}
+    __device__ __forceinline__ void tail(const Early&) const {
+        __shared__ float sv[16];
+        __shared__ int si[16];
+        float v = bv;
+        int i = bi;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(v, off, WAVE);
+            const int oi = __shfl_xor(i, off, WAVE);
+            argmax_merge(v, i, ov, oi);
+        }
+        const uint32_t wv = threadIdx.x / WAVE, nw = blockDim.x / WAVE;
+        if (threadIdx.x % WAVE == 0) {
+            sv[wv] = v;
+            si[wv] = i;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (uint32_t k = 1; k < nw; ++k) argmax_merge(v, i, sv[k], si[k]);
+            pv[blockIdx.x] = v;
+            pi[blockIdx.x] = i;
+            if (blockIdx.x == 0) *count = gridDim.x;
+        }
+    }
 };
 
 // Weights, raw scale bits and epilogue inputs of the rows one wave handles.
@@ -1051,6 +1111,32 @@ hipError_t gemv_plain(hipStream_t s, const GemvArgs& a) {
     return hipSuccess;
 }
 
+// The lm_head GEMV of one row with its argmax folded in (EpiLogitsArgmax),
+// then the reduction of the blocks' partials.  Scratch: the count (16 bytes),
+// then the partials' values and indices, room for at least one per CU (the
+// tail epilogue runs only with at most one block per CU).
+template <typename T>
+hipError_t gemv_argmax(hipStream_t s, const GemvArgs& a, int32_t* ids, void* scratch, size_t bytes) {
+    const size_t cap = bytes > 16 ? (bytes - 16) / 8 : 0;
+    if (a.M != 1 || a.wfmt != LSSM_W_DENSE || a.epi != LSSM_EPI_NONE || a.res || cap < num_cus() ||
+        (uintptr_t)scratch % 16 != 0)
+        return hipErrorNotSupported;
+    const bool norm = a.norm_w != nullptr;
+    GemvCore c{a.x, a.x_stride, (const uint8_t*)a.w, nullptr, a.norm_w, a.eps, a.N, a.K, 1.0f / (float)a.K};
+    const bool aligned = ((uintptr_t)c.x % 16 == 0) && ((c.x_stride * sizeof(T)) % 16 == 0) &&
+                         (!norm || (uintptr_t)c.norm_w % 16 == 0) && ((uintptr_t)c.w % 16 == 0);
+    if (!aligned || gemv1_rows(c.K, LSSM_W_DENSE, act_of<T>()) < 1) return hipErrorNotSupported;
+    uint32_t* count = (uint32_t*)scratch;
+    float* pv = (float*)((char*)scratch + 16);
+    int* pi = (int*)(pv + cap);
+    EpiLogitsArgmax<T> e{(T*)a.y, pv, pi, count};
+    bool done = false;
+    const hipError_t err = launch_gemv1<LSSM_W_DENSE, T, 1, EpiLogitsArgmax<T>>(s, c, e, 1, norm ? 1 : 0, done);
+    if (!done) return hipErrorNotSupported;
+    if (err != hipSuccess) return err;
+    return launch_argmax_final(s, pv, pi, count, ids);
+}
+
 // Bit-exact dequantization: out[n, k] = float(q) * float(scale).
 template <int FMT>
 __global__ void dequant_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ s,
@@ -1073,6 +1159,13 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, const uint16_t* __
 }  // namespace
 
 int gemv_max_rows(uint32_t K, int wfmt, int act) { return max_rows(K, wfmt, act); }
+
+hipError_t launch_gemv_argmax(hipStream_t s, const GemvArgs& a, int32_t* ids, void* scratch,
+                              size_t scratch_bytes) {
+    if (a.act == LSSM_F16) return gemv_argmax<f16>(s, a, ids, scratch, scratch_bytes);
+    if (a.act == LSSM_BF16) return gemv_argmax<bf16>(s, a, ids, scratch, scratch_bytes);
+    return hipErrorNotSupported;
+}
 int gemv_lds_rows(uint32_t K, int wfmt, int act) { return lds_rows(K, wfmt, act); }
 
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a) {

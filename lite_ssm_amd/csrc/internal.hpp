@@ -117,6 +117,10 @@ hipError_t launch_embed(hipStream_t s, const void* table, const int32_t* ids, vo
                         uint32_t* seq = nullptr);
 hipError_t launch_argmax(hipStream_t s, const void* logits, int32_t* ids, uint32_t rows,
                          uint32_t vocab, int act, void* scratch);
+// ids[0] = the first index of the maximum over *nblk partials (pv, pi)
+hipError_t launch_argmax_final(hipStream_t s, const float* pv, const int* pi, const uint32_t* nblk,
+                               int32_t* ids);
+
 // appends next[0..B) as row *pos of log [cap][B] and advances *pos (B <= 64)
 hipError_t launch_id_log(hipStream_t s, const int32_t* next, uint32_t B, int32_t* log, uint32_t cap,
                          uint32_t* pos);
@@ -152,6 +156,12 @@ struct GemvArgs {
     const void* ynorm_w = nullptr;
 };
 hipError_t launch_gemv(hipStream_t s, const GemvArgs& a);
+// One row of logits (dense weights, epi none) and its greedy id: the GEMV's
+// blocks write the logits and each block's (max, first index) into scratch,
+// then one block reduces them into ids[0].  hipErrorNotSupported: the shape
+// or scratch does not allow it (the caller runs launch_gemv + launch_argmax).
+hipError_t launch_gemv_argmax(hipStream_t s, const GemvArgs& a, int32_t* ids, void* scratch,
+                              size_t scratch_bytes);
 // Rows of x one GEMV launch can take for this K / format (0 = none), with
 // 16-byte aligned operands / with any alignment.
 int gemv_max_rows(uint32_t K, int wfmt, int act);

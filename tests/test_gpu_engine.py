@@ -358,6 +358,57 @@ def test_engine_prefill_folded_norms(ctx, monkeypatch):
     assert not np.array_equal(on[2], off[2]), "the second layer's rows are bit-identical: no fold ran"
 
 
+@pytest.mark.parametrize("act,wfmt", [(O.BF16, O.W_Q4_G64), (O.F16, O.W_Q8_G32)], ids=["bf16", "f16"])
+def test_engine_lm_head_argmax_fused(ctx, monkeypatch, act, wfmt):
+    """Batch 1: the lm_head launch that also reduces each block's rows to
+    (max, first index) plus one final reduction, against the two-pass argmax
+    over the stored logits (LSSM_FUSED_ARGMAX=0), at the real vocabulary (one
+    partial per block of a grid of about one block per CU).  The lm_head
+    repeats every row four times (rows 2k, 2k + 1, V/2 + 2k, V/2 + 2k + 1), so
+    the maximum is always a tie inside one block and across blocks, and the
+    first-index rule (sampler.cpp:13-21) must pick the even row below V/2."""
+    from lite_ssm_amd.model import Engine
+    L, sh, m, _ = _setup(ctx, "mamba2-130m", act, wfmt, n_layer=2, vocab_size=50280)
+    V, half = sh.vocab_size, sh.vocab_size // 2
+    m.lm_head = m.lm_head.clone()
+    m.lm_head[half:2 * half] = m.lm_head[:half]
+    m.lm_head[1:half:2] = m.lm_head[0:half - 1:2]
+    m.lm_head[half + 1:2 * half:2] = m.lm_head[half:2 * half - 1:2]
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, V, (1, 40), generator=g, dtype=torch.int32).cuda()
+
+    def run(fused):
+        monkeypatch.setenv("LSSM_FUSED_ARGMAX", "1" if fused else "0")
+        eng = Engine(ctx, m, max_batch=1, max_seq=64)
+        tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+        out, lgs = [], []
+        eng.prefill(ids, tok)
+        out.append(int(tok.item()))
+        lgs.append(eng.logits(1))
+        for _ in range(6):                       # eager, feeding back its own ids
+            eng.decode(tok, tok)
+            out.append(int(tok.item()))
+            lgs.append(eng.logits(1))
+        for _ in range(2):                       # graph replay: 1 + 4 + 1 steps, then 5
+            eng.decode_graph(tok, tok, 6)
+            out.append(int(tok.item()))
+            lgs.append(eng.logits(1))
+        eng.close()
+        return out, lgs
+
+    ids_f, lg_f = run(True)
+    ids_p, lg_p = run(False)
+    assert ids_f == ids_p
+    for a, b in zip(lg_f, lg_p):
+        assert torch.equal(a, b)
+    for i, lg in zip(ids_f, lg_f):
+        h = lg.float().cpu().numpy()[0]
+        assert i == int(np.argmax(h))            # first index of the maximum
+        assert i < half and i % 2 == 0, i
+        assert h[i] == h[i + 1] == h[half + i] == h[half + i + 1]
+
+
 def test_engine_one_token_prefill(ctx):
     """L == 1 prefill takes the reference's GEMV / conv-update / SSD-step path
     and seeds the conv state (mamba2_block.cpp:111-116, 155-162, 183-195, 285-289)."""
