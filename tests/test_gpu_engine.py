@@ -358,8 +358,12 @@ def test_engine_prefill_folded_norms(ctx, monkeypatch):
     assert not np.array_equal(on[2], off[2]), "the second layer's rows are bit-identical: no fold ran"
 
 
-@pytest.mark.parametrize("act,wfmt", [(O.BF16, O.W_Q4_G64), (O.F16, O.W_Q8_G32)], ids=["bf16", "f16"])
-def test_engine_lm_head_argmax_fused(ctx, monkeypatch, act, wfmt):
+@pytest.mark.parametrize("name,act,wfmt,vocab", [
+    ("mamba2-130m", O.BF16, O.W_Q4_G64, 50280),
+    ("mamba2-130m", O.F16, O.W_Q8_G32, 50280),
+    ("mamba2-8b", O.BF16, O.W_Q4_G64, 256000),      # config 5's lm_head: K 4096, 256000 rows
+], ids=["130m-bf16", "130m-f16", "8b-bf16"])
+def test_engine_lm_head_argmax_fused(ctx, monkeypatch, name, act, wfmt, vocab):
     """Batch 1: the lm_head launch that also reduces each block's rows to
     (max, first index) plus one final reduction, against the two-pass argmax
     over the stored logits (LSSM_FUSED_ARGMAX=0), at the real vocabulary (one
@@ -367,8 +371,9 @@ def test_engine_lm_head_argmax_fused(ctx, monkeypatch, act, wfmt):
     repeats every row four times (rows 2k, 2k + 1, V/2 + 2k, V/2 + 2k + 1), so
     the maximum is always a tie inside one block and across blocks, and the
     first-index rule (sampler.cpp:13-21) must pick the even row below V/2."""
-    from lite_ssm_amd.model import Engine
-    L, sh, m, _ = _setup(ctx, "mamba2-130m", act, wfmt, n_layer=2, vocab_size=50280)
+    from lite_ssm_amd.model import DeviceModel, Engine, shape
+    sh = shape(name, n_layer=1 if name == "mamba2-8b" else 2, vocab_size=vocab)
+    m = DeviceModel(sh, act=act, wfmt=wfmt, seed=11)
     V, half = sh.vocab_size, sh.vocab_size // 2
     m.lm_head = m.lm_head.clone()
     m.lm_head[half:2 * half] = m.lm_head[:half]
@@ -402,6 +407,7 @@ def test_engine_lm_head_argmax_fused(ctx, monkeypatch, act, wfmt):
     assert ids_f == ids_p
     for a, b in zip(lg_f, lg_p):
         assert torch.equal(a, b)
+    print(f"case: {name} vocab {V}: ids {ids_f}", flush=True)
     for i, lg in zip(ids_f, lg_f):
         h = lg.float().cpu().numpy()[0]
         assert i == int(np.argmax(h))            # first index of the maximum
