@@ -212,7 +212,7 @@ __global__ void split_silu_kernel(const T* __restrict__ xBC, T* __restrict__ xo,
 template <typename T, bool SILU>
 __global__ void conv1d_kernel(const T* __restrict__ x, uint32_t xs, const T* __restrict__ w,
                               const T* __restrict__ bias, T* __restrict__ y, uint32_t ys,
-                              uint32_t L, uint32_t D, uint32_t K) {
+                              uint32_t L, uint32_t D, uint32_t K, const T* __restrict__ hist) {
     const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
     const uint32_t t = blockIdx.y;
     const uint32_t b = blockIdx.z;
@@ -223,6 +223,7 @@ __global__ void conv1d_kernel(const T* __restrict__ x, uint32_t xs, const T* __r
         int src = (int)t - (int)(K - 1 - tap);
         float v = 0.0f;
         if (src >= 0) v = to_f(x[(row0 + (uint32_t)src) * xs + d]);
+        else if (hist) v = to_f(hist[(size_t)d * K + (K + src)]);   // the sequence's earlier rows
         acc += to_f(w[(size_t)d * K + tap]) * v;
     }
     float o = rnd<T>(acc);
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(256) void conv1d_vec_kernel(const T* __restrict__ x
                                                          const T* __restrict__ w,
                                                          const T* __restrict__ bias,
                                                          T* __restrict__ y, uint32_t ys, uint32_t L,
-                                                         uint32_t D) {
+                                                         uint32_t D, const T* __restrict__ hist) {
   if constexpr (sizeof(T) == 2) {                    // launched for fp16 / bf16 only
     const uint32_t d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
     if (d0 >= D) return;
@@ -257,6 +258,21 @@ __global__ __launch_bounds__(256) void conv1d_vec_kernel(const T* __restrict__ x
         const int t = (int)t0 + i - 3;
         win[i] = (t >= 0 && t < (int)L) ? *reinterpret_cast<const v4u*>(xb + (size_t)t * xs)
                                         : v4u{0, 0, 0, 0};
+    }
+    // rows before the first (t0 == 0 only): the sequence's earlier rows, the
+    // last K entries of each channel's conv state (entry K + t for row t < 0)
+    if (hist && t0 == 0) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            uint32_t h[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint16_t lo = __builtin_bit_cast(uint16_t, hist[(size_t)(d0 + 2 * q) * 4 + 1 + i]);
+                const uint16_t hi = __builtin_bit_cast(uint16_t, hist[(size_t)(d0 + 2 * q + 1) * 4 + 1 + i]);
+                h[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+            }
+            win[i] = v4u{h[0], h[1], h[2], h[3]};
+        }
     }
     // taps w[d][0..3] of the 8 channels: 64 contiguous bytes
     float wf[8][4], bf[8];
@@ -539,8 +555,9 @@ hipError_t launch_split_silu(hipStream_t s, const void* xBC, void* x, void* B, v
 
 hipError_t launch_conv1d(hipStream_t s, const void* x, uint32_t xs, const void* w, const void* bias,
                          void* y, uint32_t ys, uint32_t B, uint32_t L, uint32_t D, uint32_t K,
-                         int act, bool silu) {
+                         int act, bool silu, const void* hist) {
     if ((size_t)B * L * D == 0) return hipSuccess;
+    if (hist && B != 1) return hipErrorInvalidValue;
     const bool vec = act != LSSM_F32 && K == 4 && D % 8 == 0 && xs % 8 == 0 && ys % 8 == 0 &&
                      (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)w % 16 == 0 &&
                      (bias == nullptr || (uintptr_t)bias % 16 == 0);
@@ -549,11 +566,11 @@ hipError_t launch_conv1d(hipStream_t s, const void* x, uint32_t xs, const void* 
         if (silu) {
             LSSM_DISPATCH_ACT(act, T,
                               conv1d_vec_kernel<T, true><<<gv, 256, 0, s>>>((const T*)x, xs, (const T*)w,
-                                                                            (const T*)bias, (T*)y, ys, L, D));
+                                                                            (const T*)bias, (T*)y, ys, L, D, (const T*)hist));
         } else {
             LSSM_DISPATCH_ACT(act, T,
                               conv1d_vec_kernel<T, false><<<gv, 256, 0, s>>>((const T*)x, xs, (const T*)w,
-                                                                             (const T*)bias, (T*)y, ys, L, D));
+                                                                             (const T*)bias, (T*)y, ys, L, D, (const T*)hist));
         }
         return hipGetLastError();
     }
@@ -562,12 +579,12 @@ hipError_t launch_conv1d(hipStream_t s, const void* x, uint32_t xs, const void* 
         LSSM_DISPATCH_ACT(act, T,
                           conv1d_kernel<T, true><<<grid, NT, 0, s>>>((const T*)x, xs, (const T*)w,
                                                                      (const T*)bias, (T*)y, ys, L,
-                                                                     D, K));
+                                                                     D, K, (const T*)hist));
     } else {
         LSSM_DISPATCH_ACT(act, T,
                           conv1d_kernel<T, false><<<grid, NT, 0, s>>>((const T*)x, xs, (const T*)w,
                                                                       (const T*)bias, (T*)y, ys, L,
-                                                                      D, K));
+                                                                      D, K, (const T*)hist));
     }
     return hipGetLastError();
 }

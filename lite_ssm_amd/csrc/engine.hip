@@ -104,6 +104,11 @@ struct lssm_engine {
     // LSSM_SPLIT_PREFILL=0 at creation keeps one stream.
     hipStream_t side = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    // one long sequence: its two halves in time, the second on that stream a
+    // layer behind, each of its layers after the first half's scan of the
+    // layer (the SSD state and conv window it continues from): one event a
+    // layer (8B at 1 x 8192: 111.5 -> 106.4 ms)
+    std::vector<hipEvent_t> ev_layer;
     float* seg2 = nullptr;
     float* gemm_ws2 = nullptr;
     bool split_prefill = true;
@@ -203,6 +208,7 @@ struct lssm_engine {
         }
         if (ev_fork) (void)hipEventDestroy(ev_fork);
         if (ev_join) (void)hipEventDestroy(ev_join);
+        for (hipEvent_t ev : ev_layer) (void)hipEventDestroy(ev);
         for (void* p : allocs) (void)hipFree(p);
     }
 
@@ -439,17 +445,26 @@ struct lssm_engine {
         // two halves on two streams: a batch of at least 8192 rows in
         // sequences of at least 64 tokens (each half's GEMMs still fill the
         // GPU), no debug trace (it reads one stream's rows in order)
-        const uint32_t b0 = split_prefill && side && !fused && !trace && act != LSSM_F32 && B >= 2 &&
-                                    L >= 64 && R >= 8192 ? B / 2 : 0;
+        const bool can_split = split_prefill && side && !fused && !trace && act != LSSM_F32;
+        const uint32_t b0 = can_split && B >= 2 && L >= 64 && R >= 8192 ? B / 2 : 0;
+        // one sequence of at least 8192 tokens: halves in time, on chunk bounds
+        const uint32_t th = can_split && B == 1 && L >= 8192 && ev_layer.size() >= cfg.n_layer ? L / 2 / 64 * 64 : 0;
         hipError_t e;
-        if (b0 == 0) {
-            e = prefill_layers(ids, 0, B, L, ck, fused, st(), seg, gemm_ws);
+        if (b0 == 0 && th == 0) {
+            e = prefill_layers(ids, 0, B, L, 0, L, ck, fused, st(), seg, gemm_ws);
         } else {
             e = hipEventRecord(ev_fork, st());
             if (e == hipSuccess) e = hipStreamWaitEvent(side, ev_fork, 0);
             if (e != hipSuccess) return e;
-            e = prefill_layers(ids, 0, b0, L, ck, fused, st(), seg, gemm_ws);
-            if (e == hipSuccess) e = prefill_layers(ids, b0, B - b0, L, ck, fused, side, seg2, gemm_ws2);
+            if (b0) {
+                e = prefill_layers(ids, 0, b0, L, 0, L, ck, fused, st(), seg, gemm_ws);
+                if (e == hipSuccess) e = prefill_layers(ids, b0, B - b0, L, 0, L, ck, fused, side, seg2, gemm_ws2);
+            } else {
+                e = prefill_layers(ids, 0, 1, L, 0, th, ck, fused, st(), seg, gemm_ws, ev_layer.data(), nullptr);
+                if (e == hipSuccess)
+                    e = prefill_layers(ids, 0, 1, L, th, L - th, ck, fused, side, seg2, gemm_ws2, nullptr,
+                                       ev_layer.data());
+            }
             // joined whatever happened, so nothing stays queued unordered on the side stream
             hipError_t j = hipEventRecord(ev_join, side);
             if (j == hipSuccess) j = hipStreamWaitEvent(st(), ev_join, 0);
@@ -462,14 +477,18 @@ struct lssm_engine {
         return e;
     }
 
-    // The layers of a prefill for sequences b0 .. b0 + nb of the batch on
-    // stream strm (mamba2_block.cpp:296-315): rows b0 L .. of every row
-    // buffer, the sequences' conv / SSD state and Gram tiles, and the given
-    // segment and split-K workspaces.
-    hipError_t prefill_layers(const int32_t* ids, uint32_t b0, uint32_t nb, uint32_t L, uint32_t ck, bool fused,
-                              hipStream_t strm, float* segw, float* gws) const {
+    // The layers of a prefill for tokens t0 .. t0 + L of sequences b0 .. b0 +
+    // nb of the batch (sequence length Ls) on stream strm
+    // (mamba2_block.cpp:296-315): rows b0 Ls + t0 .. of every row buffer, the
+    // sequences' conv / SSD state and Gram tiles, and the given segment and
+    // split-K workspaces.  t0 > 0 (one sequence): the prefill continues from
+    // the state and conv window that tokens 0 .. t0 left, each layer after
+    // the event wait[li]; rec: an event recorded after each layer's scan.
+    hipError_t prefill_layers(const int32_t* ids, uint32_t b0, uint32_t nb, uint32_t Ls, uint32_t t0, uint32_t L,
+                              uint32_t ck, bool fused, hipStream_t strm, float* segw, float* gws,
+                              const hipEvent_t* rec = nullptr, const hipEvent_t* wait = nullptr) const {
         const uint32_t R = nb * L;
-        const size_t r0 = (size_t)b0 * L;
+        const size_t r0 = (size_t)b0 * Ls + t0;
         char* hid = (char*)hidden + r0 * d_model * es;
         char* nrm = (char*)normed + r0 * d_model * es;
         char* prj = (char*)projb + r0 * proj * es;
@@ -479,7 +498,7 @@ struct lssm_engine {
         float* grs = g_rs + r0;
         float* hrs = h_rs + r0;
         float* hp = hpart + (size_t)(d_model / 128) * r0;     // this half's [part][nb L] block
-        float* gr = gram + (size_t)b0 * ((L + 63) / 64) * G * 64 * 64;
+        float* gr = gram + ((size_t)b0 * ((Ls + 63) / 64) + t0 / 64) * G * 64 * 64;
         const size_t cofs = (size_t)b0 * xbc * K * es;
         const size_t sofs = (size_t)b0 * H * P * N;
         hipError_t e = launch_embed(strm, embed, ids + r0, hid, R, d_model, vocab, act, ctx->status);
@@ -522,14 +541,17 @@ struct lssm_engine {
                 e = short_prefill_mixer(li, nb, L, ck);   // (never split)
             } else {
                 const char* xbc_pre = prj + (size_t)d_inner * es;
-                e = launch_conv1d(strm, xbc_pre, proj, w.conv1d_w, w.conv1d_b, xba, xbc, nb, L, xbc, K,
-                                  act, true);
+                if (wait) e = hipStreamWaitEvent(strm, wait[li], 0);
+                if (e == hipSuccess)
+                    e = launch_conv1d(strm, xbc_pre, proj, w.conv1d_w, w.conv1d_b, xba, xbc, nb, L, xbc, K,
+                                      act, true, t0 ? conv_layer(li) + cofs : nullptr);
                 if (e == hipSuccess)
                     e = launch_conv1d_seed(strm, xbc_pre, proj, conv_layer(li) + cofs, nb, L, xbc, K, act);
                 if (e == hipSuccess) {
                     e = launch_ssd_chunked(strm, s);
                     if (e == hipSuccess && gparts)
                         e = launch_rms_from_parts(strm, s.gpart, gparts, R, d_inner, RMS_EPS, grs);
+                    if (e == hipSuccess && rec) e = hipEventRecord(rec[li], strm);
                 }
                 if (e == hipSuccess && !gparts)
                     e = launch_gated_rmsnorm(strm, prj, proj, yb, d_inner, w.mixer_norm_w, gnb, R, d_inner,
@@ -747,7 +769,7 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
     A((void**)&e->h_part, hpb);
     A((void**)&e->g_part, gpb);
     if (const char* v = getenv("LSSM_SPLIT_PREFILL")) e->split_prefill = v[0] != '0';
-    if (max_batch >= 2 && e->split_prefill) {
+    if ((max_batch >= 2 || max_seq >= 8192) && e->split_prefill) {
         // the second half of a split prefill: its workspaces, stream and events
         A((void**)&e->seg2, ssd_seg_floats() * sizeof(float));
         A((void**)&e->gemm_ws2, GEMM_WS_FLOATS * sizeof(float));
@@ -755,6 +777,11 @@ int lssm_engine_create(lssm_engine** out, lssm_ctx* ctx, const lssm_model_config
             hipError_t err = hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking);
             if (err == hipSuccess) err = hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming);
             if (err == hipSuccess) err = hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming);
+            for (uint32_t li = 0; max_seq >= 8192 && li < cfg->n_layer && err == hipSuccess; ++li) {
+                hipEvent_t ev = nullptr;
+                err = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+                if (err == hipSuccess) e->ev_layer.push_back(ev);
+            }
             if (err != hipSuccess) rc = set_error(LSSM_EDEVICE, "engine_create: %s", hipGetErrorString(err));
         }
     }

@@ -96,9 +96,12 @@ hipError_t launch_silu_gated(hipStream_t s, const void* x, const void* g, void* 
                              int act);
 hipError_t launch_split_silu(hipStream_t s, const void* xBC, void* x, void* B, void* C,
                              uint32_t rows, uint32_t d_inner, uint32_t GN, int act);
+// hist (one sequence only): its conv state [D][K] as launch_conv1d_seed left
+// it after the sequence's earlier tokens; rows before x are read from there
+// instead of the zero padding (a prefill continued from an earlier part)
 hipError_t launch_conv1d(hipStream_t s, const void* x, uint32_t x_stride, const void* w,
                          const void* bias, void* y, uint32_t y_stride, uint32_t B, uint32_t L,
-                         uint32_t D, uint32_t K, int act, bool silu);
+                         uint32_t D, uint32_t K, int act, bool silu, const void* hist = nullptr);
 hipError_t launch_conv1d_update(hipStream_t s, const void* x_new, void* state, const void* w,
                                 const void* bias, void* y, uint32_t B, uint32_t D, uint32_t K,
                                 int act);

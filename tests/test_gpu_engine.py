@@ -460,6 +460,50 @@ def test_engine_prefill_split_two_streams(ctx, monkeypatch):
     eng.close()
 
 
+def test_engine_prefill_split_in_time(ctx, monkeypatch):
+    """One sequence of 8192 tokens runs as two halves in time: tokens 4096 ..
+    on the engine's own stream, each layer continuing from the SSD state and
+    conv window the first half left (the conv reads its first rows' history
+    from the conv state).  Logits, greedy id and final conv / SSD state
+    against the oracle, as with one stream (LSSM_SPLIT_PREFILL=0); then two
+    teacher-forced decode steps from the split prefill's state."""
+    from lite_ssm_amd.model import Engine
+    act, wfmt = O.BF16, O.W_Q4_G64
+    L, sh, m, om = _setup(ctx, "mamba2-130m", act, wfmt, n_layer=2, vocab_size=1024)
+    B, Lq = 1, 8192
+    g = torch.Generator().manual_seed(17)
+    ids = torch.randint(0, sh.vocab_size, (B, Lq), generator=g, dtype=torch.int32)
+    conv, ssd = om.new_state(B)
+    ref = om.prefill(conv, ssd, ids.numpy())
+    engines = {}
+    for split in ("1", "0"):
+        monkeypatch.setenv("LSSM_SPLIT_PREFILL", split)
+        eng = Engine(ctx, m, max_batch=B, max_seq=Lq)
+        nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+        eng.prefill(ids.cuda(), nxt)
+        lg = eng.logits(B).float().cpu().numpy()
+        _check_logits(lg, ref, act, f"prefill split={split}")
+        assert list(nxt.cpu().numpy()) == list(np.argmax(lg, -1))
+        gconv, gssd = eng.state()
+        es, ec = max_rel(gssd.cpu().numpy(), ssd), max_rel(gconv.float().cpu().numpy(), O.from_act(conv, act))
+        print(f"case: split={split}: SSD state max-rel {es:.4f}, conv state {ec:.4f}", flush=True)
+        # as in the batch split test: the second layer's state after many
+        # tokens, through the segmented scan's fp32 segment boundaries
+        assert es < 3e-2, f"split={split}: SSD state"
+        assert ec < MAXREL[act], f"split={split}: conv state"
+        engines[split] = eng
+    engines["0"].close()
+    eng = engines["1"]
+    nxt = torch.zeros(B, dtype=torch.int32, device="cuda")
+    tok = O.argmax(ref, act)
+    for step in range(2):
+        eng.decode(torch.from_numpy(tok).cuda(), nxt)
+        ref = om.decode(conv, ssd, tok)
+        _check_logits(eng.logits(B).float().cpu().numpy(), ref, act, f"decode {step} after the split prefill")
+        tok = O.argmax(ref, act)
+    eng.close()
+
+
 def test_engine_one_token_prefill(ctx):
     """L == 1 prefill takes the reference's GEMV / conv-update / SSD-step path
     and seeds the conv state (mamba2_block.cpp:111-116, 155-162, 183-195, 285-289)."""
