@@ -158,9 +158,15 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs a) {
         }
     };
 
+    // Each column tile starts its K walk at its own step: W rows of a
+    // power-of-two pitch (8 KB for K = 4096 bf16) otherwise put every block's
+    // row segments on the same few memory channels at once.  (The order
+    // depends on the column only, not on the row tile.)
     const uint32_t KT = a.K / BK;
-    load_a(0);
-    load_b<FMT, T>(breg, a, n0, 0);
+    const uint32_t rot = KT ? blockIdx.x % KT : 0u;
+    auto kof = [&](uint32_t kt) { const uint32_t q = kt + rot; return (q >= KT ? q - KT : q) * BK; };
+    load_a(kof(0));
+    load_b<FMT, T>(breg, a, n0, kof(0));
     for (uint32_t kt = 0; kt < KT; ++kt) {
         __syncthreads();
 #pragma unroll
@@ -171,8 +177,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs a) {
         store_b<FMT, T>(breg, Bs);
         __syncthreads();
         if (kt + 1 < KT) {
-            load_a((kt + 1) * BK);
-            load_b<FMT, T>(breg, a, n0, (kt + 1) * BK);
+            load_a(kof(kt + 1));
+            load_b<FMT, T>(breg, a, n0, kof(kt + 1));
         }
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
