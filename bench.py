@@ -240,8 +240,9 @@ def bench_ref_api(L, torch, ctx, timer, n_new=33, prompt_len=64):
     generate(); tests/cpp/_bin/ref_model_run, built from the reference sources
     against include/lite_ssm/*.hpp) on this backend, greedy decode of a
     130M-shaped int4-b32 / fp16 file, the reference's formats.  Its activations
-    and state live in DeviceBuffers of pinned host memory, so every kernel reaches
-    them over PCIe and every op is a host round trip.  Beside it, the engine on
+    and state live in DeviceBuffers in HBM whose host views are synchronised at
+    op boundaries; every op is its own launch (and, outside the model's
+    batches, a host round trip).  Beside it, the engine on
     the same file (HBM-resident, one graph launch per four steps).  None when the
     harness was not built (it needs the reference checkout at build time)."""
     import subprocess

@@ -6,10 +6,14 @@
 // model layer compiles unchanged against it.  On a discrete MI355X:
 //
 //   MmapFile      POSIX mmap(PROT_READ, MAP_PRIVATE) of a whole file.
-//   DeviceBuffer  pinned, coherent host memory mapped into the GPU
-//                 (hipHostMalloc): contents() is the CPU view the model layer
-//                 memcpy's into (embed) and reads logits from; metal_buffer()
-//                 is the same address, used by kernels over PCIe.
+//   DeviceBuffer  HBM (metal_buffer(), the kernels' pointer) with a host
+//                 mirror as contents(): the CPU view the model layer memcpy's
+//                 into (embed) and reads logits from.  Mirror pages are
+//                 brought in from HBM when the host touches them and written
+//                 back before the next op that names the buffer, so the host
+//                 sees the GPU's writes once that work has finished, as with
+//                 the reference's shared buffers.  An inaccessible mirror page
+//                 must be touched before it is passed to a system call.
 //   UnifiedBuffer the weights: an HBM copy of the mapping uploaded once;
 //                 contents() stays the mmap base (reference contract,
 //                 tests/test_mmap_loader.cpp:99-103), metal_buffer() is the

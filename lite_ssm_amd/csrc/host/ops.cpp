@@ -11,6 +11,7 @@
 
 #include "lite_ssm/ops.hpp"
 #include "lssm.h"
+#include "mirror.hpp"
 
 #include <cstdint>
 #include <stdexcept>
@@ -41,8 +42,20 @@ template <class P>
 inline P* at(MetalBufferHandle h, std::size_t off) {
     return h ? reinterpret_cast<P*>(static_cast<std::uint8_t*>(h) + off) : nullptr;
 }
-inline const void* cv(MetalBufferHandle h, std::size_t off) { return at<const void>(h, off); }
-inline void* mv(MetalBufferHandle h, std::size_t off) { return at<void>(h, off); }
+// every buffer an op names is brought up to date on the device first (the
+// host's writes uploaded, its host view invalidated: allocator.cpp)
+inline const void* cv(MetalBufferHandle h, std::size_t off) {
+    detail::mirror_sync_for_device(h);
+    return at<const void>(h, off);
+}
+inline void* mv(MetalBufferHandle h, std::size_t off) {
+    detail::mirror_sync_for_device(h);
+    return at<void>(h, off);
+}
+inline float* fv(MetalBufferHandle h, std::size_t off) {
+    detail::mirror_sync_for_device(h);
+    return at<float>(h, off);
+}
 
 }  // namespace
 
@@ -220,7 +233,7 @@ void MetalOps::ssd_chunked_f16(MetalBufferHandle X, std::size_t X_off, MetalBuff
     check(lssm_ssd_chunked_f16(
         impl_->get(), cv(X, X_off), cv(B, B_off), cv(C, C_off), cv(dt_raw, dt_off),
         cv(dt_bias, db_off), cv(A_log, A_off), cv(D_skip, D_off), mv(Y, Y_off),
-        at<float>(state_io, S_off),
+        fv(state_io, S_off),
         lssm_ssd_dims{d.L, d.H, d.P, d.N, d.n_groups, d.chunk_size, d.dt_min, d.dt_max, d.has_D}));
 }
 
@@ -234,7 +247,7 @@ void MetalOps::ssd_step_f16(MetalBufferHandle x, std::size_t x_off, MetalBufferH
                             MetalBufferHandle y, std::size_t y_off, SSDStepDims d) {
     check(lssm_ssd_step_f16(
         impl_->get(), cv(x, x_off), cv(B, B_off), cv(C, C_off), cv(dt_raw, dt_off),
-        cv(dt_bias, db_off), cv(A_log, A_off), cv(D_skip, D_off), at<float>(state, S_off),
+        cv(dt_bias, db_off), cv(A_log, A_off), cv(D_skip, D_off), fv(state, S_off),
         mv(y, y_off),
         lssm_ssd_step_dims{d.H, d.P, d.N, d.n_groups, d.dt_min, d.dt_max, d.has_D}));
 }

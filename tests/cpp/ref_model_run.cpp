@@ -57,6 +57,15 @@ int main(int argc, char** argv) {
         lite_ssm::GenerationConfig gc;
         gc.max_new_tokens = n_new;
         gc.greedy = true;
+        // one untimed generation first (each kernel's code is loaded on its
+        // first launch), as the reference's benchmark drops its first
+        // iteration (examples/benchmark_litessm.cpp); generate() resets the
+        // state, so the timed run starts from the same place
+        {
+            lite_ssm::GenerationConfig warm = gc;
+            warm.max_new_tokens = 2;
+            lite_ssm::generate(model, ops, ws, state, prompt, warm, [](uint32_t) {});
+        }
         // the callback runs right after each pick, while the workspace's fp32
         // scratch still holds the logits the id was taken from
         using clk = std::chrono::steady_clock;

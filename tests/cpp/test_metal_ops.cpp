@@ -230,6 +230,64 @@ int main() {
         EXPECT(es < 1e-3, "ssd_step state max-rel %.3g", es);
     }
 
+    // --- 6. DeviceBuffer's host view (HBM storage, page-protected mirror) ---
+    // host writes reach the op, the op's writes reach later host reads, over
+    // pages brought in as windows, rewritten after a read, cleared by zero(),
+    // across two buffers and after a move
+    {
+        const uint32_t n = 20000;                     // 40 KB per fp16 vector: 10 pages
+        const std::size_t pg = (std::size_t)sysconf(_SC_PAGESIZE);
+        lite_ssm::DeviceBuffer buf(3 * n * 2 + 6);    // not a whole number of pages
+        bool zero0 = true;                            // a new buffer reads as zeros
+        for (uint32_t i = 0; i < 3 * n; ++i) zero0 = zero0 && host<uint16_t>(buf)[i] == 0;
+        EXPECT(zero0, "new DeviceBuffer reads zero");
+        for (int round = 0; round < 3; ++round) {
+            auto a = rand_f16(n, -4.f, 4.f), b = rand_f16(n, -1.f, 1.f);
+            // round 1 rewrites pages the host has just read (clean -> dirty);
+            // round 2 writes one element per page only, the rest stays as read
+            if (round < 2) {
+                std::memcpy(host<uint16_t>(buf), a.data(), n * 2);
+                std::memcpy(host<uint16_t>(buf) + n, b.data(), n * 2);
+            } else {
+                for (uint32_t i = 0; i < n; ++i) {
+                    a[i] = host<uint16_t>(buf)[i];
+                    b[i] = host<uint16_t>(buf)[n + i];
+                }
+                for (uint32_t i = 0; i < n; i += (uint32_t)(pg / 2)) {
+                    a[i] = orc_f2h(0.5f + i % 7);
+                    host<uint16_t>(buf)[i] = a[i];
+                }
+            }
+            ops.silu_f16(buf.metal_buffer(), 0, buf.metal_buffer(), 2 * n * 2, n);
+            ops.add_inplace_f16(buf.metal_buffer(), 2 * n * 2, buf.metal_buffer(), n * 2, n);
+            std::vector<uint16_t> ref(n);
+            orc_silu(a.data(), ref.data(), n, LSSM_F16);
+            orc_add_inplace(ref.data(), b.data(), n, LSSM_F16);
+            const double e = max_rel16(host<uint16_t>(buf) + 2 * n, ref.data(), n);
+            EXPECT(e < 2e-2, "host view round %d: silu+add max-rel %.3g", round, e);
+        }
+        // the last bytes, past the last whole page, round-trip too
+        host<uint8_t>(buf)[3 * n * 2 + 5] = 0xA5;
+        ops.silu_f16(buf.metal_buffer(), 0, buf.metal_buffer(), 2 * n * 2, 1);
+        EXPECT(host<uint8_t>(buf)[3 * n * 2 + 5] == 0xA5, "tail byte kept across an op");
+        buf.zero();
+        bool zeroed = true;
+        for (uint32_t i = 0; i < 3 * n; ++i) zeroed = zeroed && host<uint16_t>(buf)[i] == 0;
+        EXPECT(zeroed, "zero() clears what the host sees");
+        // two buffers: input in one, output in the other; then the buffer moved
+        lite_ssm::DeviceBuffer in(n * 2), out(n * 2);
+        auto a = rand_f16(n, -4.f, 4.f);
+        std::memcpy(host<uint16_t>(in), a.data(), n * 2);
+        std::memset(host<uint16_t>(out), 0x3C, n * 2);     // overwritten by the op
+        ops.silu_f16(in.metal_buffer(), 0, out.metal_buffer(), 0, n);
+        lite_ssm::DeviceBuffer moved(std::move(out));
+        std::vector<uint16_t> ref(n);
+        orc_silu(a.data(), ref.data(), n, LSSM_F16);
+        const double e = max_rel16(host<uint16_t>(moved), ref.data(), n);
+        EXPECT(e < 2e-2, "two buffers: silu max-rel %.3g", e);
+        EXPECT(std::memcmp(host<uint16_t>(in), a.data(), n * 2) == 0, "input kept");
+    }
+
     if (g_fail) {
         std::fprintf(stderr, "[test_metal_ops] FAIL: %d check(s)\n", g_fail);
         return 1;
