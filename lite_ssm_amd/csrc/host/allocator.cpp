@@ -60,13 +60,17 @@ enum : std::uint8_t { PAGE_INVALID = 0, PAGE_CLEAN = 1, PAGE_DIRTY = 2 };
 constexpr int         kSlots  = 1024;   // live DeviceBuffers
 constexpr std::size_t kWindow = 16;     // pages copied in per fault
 
+// A registry entry.  Entries are never freed, only reused, so a lookup that
+// races with another buffer's destruction reads a live object; every use
+// re-checks `live` and the addresses under `mu`.
 struct Mirror {
-    char*         host   = nullptr;     // mmap'd, npages * page bytes
-    char*         dev    = nullptr;     // lssm_malloc'd, same size
-    std::size_t   npages = 0;
-    std::size_t   nvalid = 0;           // pages not PAGE_INVALID
-    std::uint8_t* st     = nullptr;     // per page state
-    std::mutex    mu;
+    std::atomic<bool>        live{false};
+    std::atomic<char*>       host{nullptr};    // mmap'd, npages * page bytes
+    std::atomic<char*>       dev{nullptr};     // lssm_malloc'd, same size
+    std::atomic<std::size_t> npages{0};
+    std::size_t              nvalid = 0;       // pages not PAGE_INVALID (under mu)
+    std::uint8_t*            st     = nullptr; // per page state (under mu)
+    std::mutex               mu;
 };
 
 std::atomic<Mirror*> g_slot[kSlots];
@@ -83,10 +87,16 @@ bool copy(void* dst, const void* src, std::size_t n, bool to_device) {
     return (to_device ? lssm_memcpy_h2d(g_ctx, dst, src, n) : lssm_memcpy_d2h(g_ctx, dst, src, n)) == LSSM_OK;
 }
 
+bool holds(const Mirror& m, const char* a) {
+    const char* h = m.host.load(std::memory_order_acquire);
+    return m.live.load(std::memory_order_acquire) && h && a >= h &&
+           a < h + m.npages.load(std::memory_order_acquire) * g_page;
+}
+
 Mirror* find_host(const char* a) {
     for (auto& sl : g_slot) {
         Mirror* m = sl.load(std::memory_order_acquire);
-        if (m && a >= m->host && a < m->host + m->npages * g_page) return m;
+        if (m && holds(*m, a)) return m;
     }
     return nullptr;
 }
@@ -94,7 +104,7 @@ Mirror* find_host(const char* a) {
 Mirror* find_dev(const void* d) {
     for (auto& sl : g_slot) {
         Mirror* m = sl.load(std::memory_order_acquire);
-        if (m && m->dev == d) return m;
+        if (m && m->live.load(std::memory_order_acquire) && m->dev.load(std::memory_order_acquire) == d) return m;
     }
     return nullptr;
 }
@@ -107,7 +117,7 @@ void invalidate(Mirror& m, std::size_t a, std::size_t b) {
         m.st[i] = PAGE_INVALID;
     }
     if (n) {
-        mprotect(m.host + a * g_page, (b - a) * g_page, PROT_NONE);
+        mprotect(m.host.load() + a * g_page, (b - a) * g_page, PROT_NONE);
         m.nvalid -= n;
         g_valid.fetch_sub((long)n, std::memory_order_acq_rel);
     }
@@ -115,15 +125,17 @@ void invalidate(Mirror& m, std::size_t a, std::size_t b) {
 
 // The host touched page p of m: bring it (and up to kWindow - 1 following
 // invalid pages) in from HBM; a write makes page p writable and dirty.
-bool fault_in(Mirror& m, std::size_t p, bool write) {
+bool fault_in(Mirror& m, const char* a, bool write) {
     std::lock_guard<std::mutex> lk(m.mu);
-    char* h = m.host + p * g_page;
+    if (!holds(m, a)) return false;   // destroyed meanwhile: not a mirror access any more
+    const std::size_t p = (std::size_t)(a - m.host.load()) / g_page, np = m.npages.load();
+    char* h = m.host.load() + p * g_page;
     if (m.st[p] == PAGE_INVALID) {
         std::size_t e = p;
-        while (e < m.npages && e - p < kWindow && m.st[e] == PAGE_INVALID) ++e;
+        while (e < np && e - p < kWindow && m.st[e] == PAGE_INVALID) ++e;
         const std::size_t n = (e - p) * g_page;
         if (mprotect(h, n, PROT_READ | PROT_WRITE) != 0) return false;
-        if (!copy(h, m.dev + p * g_page, n, false)) {
+        if (!copy(h, m.dev.load() + p * g_page, n, false)) {
             mprotect(h, n, PROT_NONE);
             return false;
         }
@@ -151,8 +163,7 @@ void on_segv(int sig, siginfo_t* si, void* uc) {
 #if defined(__x86_64__)
         write = (static_cast<ucontext_t*>(uc)->uc_mcontext.gregs[REG_ERR] & 2) != 0;
 #endif
-        const std::size_t p = (std::size_t)(static_cast<const char*>(si->si_addr) - m->host) / g_page;
-        if (fault_in(*m, p, write)) return;   // the access runs again
+        if (fault_in(*m, static_cast<const char*>(si->si_addr), write)) return;   // the access runs again
     }
     // not a mirror page (or its copy failed): the previous disposition
     if (g_prev.sa_flags & SA_SIGINFO) {
@@ -203,19 +214,21 @@ void mirror_sync_for_device(const void* handle) {
     Mirror* m = find_dev(handle);
     if (!m) return;
     std::lock_guard<std::mutex> lk(m->mu);
-    if (m->nvalid == 0) return;
-    for (std::size_t i = 0; i < m->npages;) {
+    if (!m->live.load() || m->dev.load() != handle || m->nvalid == 0) return;
+    const std::size_t np = m->npages.load();
+    char *dev = m->dev.load(), *host = m->host.load();
+    for (std::size_t i = 0; i < np;) {
         if (m->st[i] != PAGE_DIRTY) {
             ++i;
             continue;
         }
         std::size_t e = i;
-        while (e < m->npages && m->st[e] == PAGE_DIRTY) ++e;
-        if (!copy(m->dev + i * g_page, m->host + i * g_page, (e - i) * g_page, true))
+        while (e < np && m->st[e] == PAGE_DIRTY) ++e;
+        if (!copy(dev + i * g_page, host + i * g_page, (e - i) * g_page, true))
             throw_lssm("DeviceBuffer: upload of host writes");
         i = e;
     }
-    invalidate(*m, 0, m->npages);
+    invalidate(*m, 0, np);
 }
 
 }  // namespace detail
@@ -226,33 +239,51 @@ void mirror_sync_for_device(const void* handle) {
 DeviceBuffer::DeviceBuffer(std::size_t nbytes) {
     if (nbytes == 0) return;
     init_mirrors();
-    auto* m   = new Mirror;
-    m->npages = (nbytes + g_page - 1) / g_page;
-    const std::size_t bytes = m->npages * g_page;
+    const std::size_t np = (nbytes + g_page - 1) / g_page, bytes = np * g_page;
     void* h = mmap(nullptr, bytes, PROT_NONE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+    if (h == MAP_FAILED) throw std::runtime_error("DeviceBuffer: mmap of the host view failed");
     void* d = nullptr;
-    const bool ok = h != MAP_FAILED && lssm_malloc(&d, bytes) == LSSM_OK && d &&
-                    lssm_memset(g_ctx, d, 0, bytes) == LSSM_OK;   // zero-filled, like a new shared buffer
-    int slot = -1;
-    if (ok) {
-        m->host = static_cast<char*>(h);
-        m->dev  = static_cast<char*>(d);
-        m->st   = new std::uint8_t[m->npages]();
-        for (int i = 0; i < kSlots && slot < 0; ++i) {
-            Mirror* expect = nullptr;
-            if (g_slot[i].compare_exchange_strong(expect, m, std::memory_order_acq_rel)) slot = i;
-        }
+    bool ok = lssm_malloc(&d, bytes) == LSSM_OK && d;
+    if (ok) {   // zero-filled, like a new shared buffer
+        std::lock_guard<std::mutex> lc(g_ctx_mu);
+        ok = lssm_memset(g_ctx, d, 0, bytes) == LSSM_OK;
     }
-    if (slot < 0) {
-        const std::string why = ok ? "more than 1024 live DeviceBuffers" : lssm_last_error();
+    if (!ok) {
+        const std::string why = lssm_last_error();
         if (d) lssm_free(d);
-        if (h != MAP_FAILED) munmap(h, bytes);
-        delete[] m->st;
-        delete m;
+        munmap(h, bytes);
         throw std::runtime_error("DeviceBuffer: " + why);
     }
-    buffer_   = m->dev;
-    contents_ = m->host;
+    // an entry not in use (reused), else a new one in an empty slot
+    Mirror* m = nullptr;
+    for (int i = 0; i < kSlots && !m; ++i) {
+        Mirror* e = g_slot[i].load(std::memory_order_acquire);
+        if (!e) {
+            auto* fresh = new Mirror;
+            fresh->live.store(true);
+            Mirror* expect = nullptr;
+            if (g_slot[i].compare_exchange_strong(expect, fresh, std::memory_order_acq_rel)) m = fresh;
+            else delete fresh;
+        } else {
+            bool expect = false;
+            if (e->live.compare_exchange_strong(expect, true, std::memory_order_acq_rel)) m = e;
+        }
+    }
+    if (!m) {
+        lssm_free(d);
+        munmap(h, bytes);
+        throw std::runtime_error("DeviceBuffer: more than 1024 live DeviceBuffers");
+    }
+    {
+        std::lock_guard<std::mutex> lk(m->mu);
+        m->st     = new std::uint8_t[np]();
+        m->nvalid = 0;
+        m->npages.store(np, std::memory_order_release);
+        m->dev.store(static_cast<char*>(d), std::memory_order_release);
+        m->host.store(static_cast<char*>(h), std::memory_order_release);
+    }
+    buffer_   = d;
+    contents_ = h;
     length_   = nbytes;
 }
 
@@ -283,25 +314,27 @@ void DeviceBuffer::zero() {
     int rc;
     {
         std::lock_guard<std::mutex> lc(g_ctx_mu);
-        rc = lssm_memset(g_ctx, m->dev, 0, m->npages * g_page);
+        rc = lssm_memset(g_ctx, m->dev.load(), 0, m->npages.load() * g_page);
     }
     if (rc != LSSM_OK) throw_lssm("DeviceBuffer::zero");
-    invalidate(*m, 0, m->npages);
+    invalidate(*m, 0, m->npages.load());
 }
 
 void DeviceBuffer::reset_() noexcept {
     if (buffer_) {
-        for (auto& sl : g_slot) {
-            Mirror* m = sl.load(std::memory_order_acquire);
-            if (m && m->dev == buffer_) {
-                sl.store(nullptr, std::memory_order_release);
-                g_valid.fetch_sub((long)m->nvalid, std::memory_order_acq_rel);
-                munmap(m->host, m->npages * g_page);
-                lssm_free(m->dev);
-                delete[] m->st;
-                delete m;
-                break;
-            }
+        if (Mirror* m = find_dev(buffer_)) {
+            std::lock_guard<std::mutex> lk(m->mu);
+            const std::size_t np = m->npages.load();
+            m->live.store(false, std::memory_order_release);
+            g_valid.fetch_sub((long)m->nvalid, std::memory_order_acq_rel);
+            munmap(m->host.load(), np * g_page);
+            lssm_free(m->dev.load());
+            delete[] m->st;
+            m->st     = nullptr;
+            m->nvalid = 0;
+            m->host.store(nullptr);
+            m->dev.store(nullptr);
+            m->npages.store(0);
         }
     }
     buffer_ = contents_ = nullptr;
