@@ -13,6 +13,7 @@ extern "C" {
 }
 
 #include <array>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -23,6 +24,7 @@ extern "C" {
 #include <stdexcept>
 #include <string>
 #include <string_view>
+#include <thread>
 #include <unistd.h>
 #include <vector>
 
@@ -286,6 +288,40 @@ int main() {
         const double e = max_rel16(host<uint16_t>(moved), ref.data(), n);
         EXPECT(e < 2e-2, "two buffers: silu max-rel %.3g", e);
         EXPECT(std::memcmp(host<uint16_t>(in), a.data(), n * 2) == 0, "input kept");
+    }
+
+    // --- 7. host views from several threads at once: each thread its own
+    // MetalOps, buffers created, written, run, read and destroyed in a loop
+    // (registry entries reused while other threads look them up)
+    {
+        constexpr int kThreads = 4, kIters = 12;
+        std::atomic<int> bad{0};
+        std::vector<std::thread> th;
+        for (int t = 0; t < kThreads; ++t) {
+            th.emplace_back([t, &bad] {
+                try {
+                    lite_ssm::MetalOps tops;
+                    std::mt19937 r(100 + t);
+                    std::uniform_real_distribution<float> u(-4.f, 4.f);
+                    for (int it = 0; it < kIters; ++it) {
+                        const uint32_t n = 3000 + 1000 * (uint32_t)((t + it) % 5);
+                        std::vector<uint16_t> a(n), ref(n);
+                        for (auto& e : a) e = orc_f2h(u(r));
+                        lite_ssm::DeviceBuffer b(2 * n * 2);
+                        std::memcpy(b.contents(), a.data(), n * 2);
+                        tops.silu_f16(b.metal_buffer(), 0, b.metal_buffer(), n * 2, n);
+                        orc_silu(a.data(), ref.data(), n, LSSM_F16);
+                        if (max_rel16(static_cast<const uint16_t*>(b.contents()) + n, ref.data(), n) >= 2e-2)
+                            bad.fetch_add(1);
+                    }
+                } catch (const std::exception& e) {
+                    std::fprintf(stderr, "thread %d: %s\n", t, e.what());
+                    bad.fetch_add(1);
+                }
+            });
+        }
+        for (auto& x : th) x.join();
+        EXPECT(bad.load() == 0, "%d of %d threaded rounds wrong", bad.load(), kThreads * kIters);
     }
 
     if (g_fail) {
