@@ -142,9 +142,10 @@ int lssm_kernel_count(void);
 const char* lssm_kernel_name(int i);
 
 /* Device memory plumbing (DeviceBuffer bodies, metal_buffer.mm:107-143).
- * lssm_malloc: HBM.  lssm_malloc_host: pinned, coherent host memory that
- * kernels read and write in place over PCIe (the shared-storage buffers of
- * the reference's model layer); release it with lssm_free_host. */
+ * lssm_malloc: HBM (DeviceBuffer's storage, and UnifiedBuffer's copy of the
+ * weights).  lssm_malloc_host: pinned, coherent host memory that kernels
+ * read and write in place over PCIe, for callers that want one address on
+ * both sides; release it with lssm_free_host. */
 int lssm_malloc(void** out, size_t nbytes);
 int lssm_malloc_host(void** out, size_t nbytes);
 int lssm_free(void* p);
