@@ -243,11 +243,11 @@ int main() {
         bool zero0 = true;                            // a new buffer reads as zeros
         for (uint32_t i = 0; i < 3 * n; ++i) zero0 = zero0 && host<uint16_t>(buf)[i] == 0;
         EXPECT(zero0, "new DeviceBuffer reads zero");
-        for (int round = 0; round < 3; ++round) {
+        for (int pass = 0; pass < 3; ++pass) {
             auto a = rand_f16(n, -4.f, 4.f), b = rand_f16(n, -1.f, 1.f);
-            // round 1 rewrites pages the host has just read (clean -> dirty);
-            // round 2 writes one element per page only, the rest stays as read
-            if (round < 2) {
+            // pass 1 rewrites pages the host has just read (clean -> dirty);
+            // pass 2 writes one element per page only, the rest stays as read
+            if (pass < 2) {
                 std::memcpy(host<uint16_t>(buf), a.data(), n * 2);
                 std::memcpy(host<uint16_t>(buf) + n, b.data(), n * 2);
             } else {
@@ -266,7 +266,7 @@ int main() {
             orc_silu(a.data(), ref.data(), n, LSSM_F16);
             orc_add_inplace(ref.data(), b.data(), n, LSSM_F16);
             const double e = max_rel16(host<uint16_t>(buf) + 2 * n, ref.data(), n);
-            EXPECT(e < 2e-2, "host view round %d: silu+add max-rel %.3g", round, e);
+            EXPECT(e < 2e-2, "host view pass %d: silu+add max-rel %.3g", pass, e);
         }
         // the last bytes, past the last whole page, round-trip too
         host<uint8_t>(buf)[3 * n * 2 + 5] = 0xA5;
@@ -321,7 +321,7 @@ int main() {
             });
         }
         for (auto& x : th) x.join();
-        EXPECT(bad.load() == 0, "%d of %d threaded rounds wrong", bad.load(), kThreads * kIters);
+        EXPECT(bad.load() == 0, "%d of %d threaded iterations wrong", bad.load(), kThreads * kIters);
     }
 
     if (g_fail) {
