@@ -109,18 +109,18 @@ Mirror* find_dev(const void* d) {
     return nullptr;
 }
 
-// make pages [a, b) of m inaccessible (caller holds m.mu)
+// make pages [a, b) of m inaccessible (caller holds m.mu); a failure (the
+// process out of memory mappings) is an error, not a stale host view
 void invalidate(Mirror& m, std::size_t a, std::size_t b) {
     std::size_t n = 0;
-    for (std::size_t i = a; i < b; ++i) {
+    for (std::size_t i = a; i < b; ++i)
         if (m.st[i] != PAGE_INVALID) ++n;
-        m.st[i] = PAGE_INVALID;
-    }
-    if (n) {
-        mprotect(m.host.load() + a * g_page, (b - a) * g_page, PROT_NONE);
-        m.nvalid -= n;
-        g_valid.fetch_sub((long)n, std::memory_order_acq_rel);
-    }
+    if (n == 0) return;
+    if (mprotect(m.host.load() + a * g_page, (b - a) * g_page, PROT_NONE) != 0)
+        throw std::runtime_error("DeviceBuffer: cannot protect the host view (mprotect failed)");
+    for (std::size_t i = a; i < b; ++i) m.st[i] = PAGE_INVALID;
+    m.nvalid -= n;
+    g_valid.fetch_sub((long)n, std::memory_order_acq_rel);
 }
 
 // The host touched page p of m: bring it (and up to kWindow - 1 following
@@ -157,6 +157,10 @@ bool fault_in(Mirror& m, const char* a, bool write) {
     return true;   // (already writable: another thread brought it in)
 }
 
+// A fault on a mirror page is synchronous: the faulting thread's own load or
+// store in code outside this library (the library touches mirror pages only
+// after making them accessible).  So the handler may take the mirror's lock
+// and call HIP as that thread could at that instruction.
 void on_segv(int sig, siginfo_t* si, void* uc) {
     if (Mirror* m = find_host(static_cast<const char*>(si->si_addr))) {
         bool write = true;   // (without the fault's error code every touch counts as a write)
