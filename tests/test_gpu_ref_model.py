@@ -38,12 +38,28 @@ def _margin_ok(ref_row, err_abs):
 
 @pytest.mark.parametrize("tag,wfmt,L", CASES, ids=[c[0] for c in CASES])
 def test_reference_model_layer_on_this_backend(ctx, tmp_path, tag, wfmt, L):
+    from lite_ssm_amd.model import shape
+    _ref_case(ctx, tmp_path, tag, shape("mamba2-130m", n_layer=4, vocab_size=4096), wfmt, L)
+
+
+# The headline model's width (d_model 2560, 80 heads) in the reference's
+# quantized format: 4 layers with the chunked scan, and all 64 layers (a
+# 167 MB SSM state in one DeviceBuffer, 1.4 GB of weights) with a short prompt.
+CASES_2P7B = [("2p7b-4layers-L40", 4, 40), ("2p7b-64layers-L12", 64, 12)]
+
+
+@pytest.mark.parametrize("tag,n_layer,L", CASES_2P7B, ids=[c[0] for c in CASES_2P7B])
+def test_reference_model_layer_2p7b_width(ctx, tmp_path, tag, n_layer, L):
+    from lite_ssm_amd.model import shape
+    _ref_case(ctx, tmp_path, tag, shape("mamba2-2.7b", n_layer=n_layer, vocab_size=4096), O.W_Q4_B32, L)
+
+
+def _ref_case(ctx, tmp_path, tag, sh, wfmt, L):
     from lite_ssm_amd import ssm as S
-    from lite_ssm_amd.model import Engine, shape
+    from lite_ssm_amd.model import Engine
     if not os.path.exists(EXE):
         pytest.skip("tests/cpp/_bin/ref_model_run not built (needs the reference checkout at build time)")
     print(f"case: reference model layer {tag}", flush=True)
-    sh = shape("mamba2-130m", n_layer=4, vocab_size=4096)
     p = tmp_path / "m.ssm"
     S.write_random(p, sh, O.F16, wfmt, seed=17)
     n_new = 8
