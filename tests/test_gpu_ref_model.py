@@ -42,16 +42,18 @@ def test_reference_model_layer_on_this_backend(ctx, tmp_path, tag, wfmt, L):
     _ref_case(ctx, tmp_path, tag, shape("mamba2-130m", n_layer=4, vocab_size=4096), wfmt, L)
 
 
-# The headline model's width (d_model 2560, 80 heads) in the reference's
-# quantized format: 4 layers with the chunked scan, and all 64 layers (a
-# 167 MB SSM state in one DeviceBuffer, 1.4 GB of weights) with a short prompt.
-CASES_2P7B = [("2p7b-4layers-L40", 4, 40), ("2p7b-64layers-L12", 64, 12)]
+# The larger BASELINE widths in the reference's quantized format: the headline
+# model's (d_model 2560, 80 heads) at 4 layers with the chunked scan and at all
+# 64 (a 167 MB SSM state in one DeviceBuffer, 1.4 GB of weights) with a short
+# prompt; the 8B's (d_model 4096, 128 heads, 8 groups of B / C) at 4 layers.
+CASES_WIDE = [("2p7b-4layers-L40", "mamba2-2.7b", 4, 40), ("2p7b-64layers-L12", "mamba2-2.7b", 64, 12),
+              ("8b-4layers-L40", "mamba2-8b", 4, 40)]
 
 
-@pytest.mark.parametrize("tag,n_layer,L", CASES_2P7B, ids=[c[0] for c in CASES_2P7B])
-def test_reference_model_layer_2p7b_width(ctx, tmp_path, tag, n_layer, L):
+@pytest.mark.parametrize("tag,name,n_layer,L", CASES_WIDE, ids=[c[0] for c in CASES_WIDE])
+def test_reference_model_layer_wide(ctx, tmp_path, tag, name, n_layer, L):
     from lite_ssm_amd.model import shape
-    _ref_case(ctx, tmp_path, tag, shape("mamba2-2.7b", n_layer=n_layer, vocab_size=4096), O.W_Q4_B32, L)
+    _ref_case(ctx, tmp_path, tag, shape(name, n_layer=n_layer, vocab_size=4096), O.W_Q4_B32, L)
 
 
 def _ref_case(ctx, tmp_path, tag, sh, wfmt, L):
