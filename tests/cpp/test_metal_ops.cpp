@@ -290,6 +290,30 @@ int main() {
         EXPECT(std::memcmp(host<uint16_t>(in), a.data(), n * 2) == 0, "input kept");
     }
 
+    // --- 8. repeated batches, as the model layer's decode steps issue them:
+    // the same ops on the same buffers with new host data each time, and
+    // batches of other sizes in between, every result checked
+    {
+        const uint32_t n = 6000;
+        lite_ssm::DeviceBuffer buf(3 * n * 2);
+        const uint32_t sizes[] = {n, n, n, n, n, n / 2, n / 2, n, n, n, n};
+        for (std::size_t it = 0; it < sizeof(sizes) / sizeof(sizes[0]); ++it) {
+            const uint32_t m = sizes[it];
+            auto a = rand_f16(m, -4.f, 4.f), b = rand_f16(m, -1.f, 1.f);
+            std::memcpy(host<uint16_t>(buf), a.data(), m * 2);
+            std::memcpy(host<uint16_t>(buf) + n, b.data(), m * 2);
+            ops.begin_batch();
+            ops.silu_f16(buf.metal_buffer(), 0, buf.metal_buffer(), 2 * n * 2, m);
+            ops.add_inplace_f16(buf.metal_buffer(), 2 * n * 2, buf.metal_buffer(), n * 2, m);
+            ops.commit_and_wait();
+            std::vector<uint16_t> ref(m);
+            orc_silu(a.data(), ref.data(), m, LSSM_F16);
+            orc_add_inplace(ref.data(), b.data(), m, LSSM_F16);
+            const double e = max_rel16(host<uint16_t>(buf) + 2 * n, ref.data(), m);
+            EXPECT(e < 2e-2, "repeated batch %zu (n %u): silu+add max-rel %.3g", it, m, e);
+        }
+    }
+
     // --- 7. host views from several threads at once: each thread its own
     // MetalOps, buffers created, written, run, read and destroyed in a loop
     // (registry entries reused while other threads look them up)
